@@ -1,0 +1,224 @@
+"""numpy front end of the CPU oracle (oracle/liborc.so).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, the smoke check and the CPU-baseline
+leg of bench.py as the checker.  The product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liborc.so"
+
+ROPE_REFERENCE, ROPE_ABSOLUTE, ROPE_NONE = 0, 1, 2
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+class OrcWindow(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("t0", "t1", "h0", "h1", "w0", "w1")]
+
+
+class OrcAttnCfg(ctypes.Structure):
+    _fields_ = [
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("eps", ctypes.c_float),
+        ("qk_norm", ctypes.c_int),
+        ("rope_mode", ctypes.c_int),
+        ("freqs", ctypes.c_void_p),
+        ("rope_theta", ctypes.c_float),
+        ("gq_vid", ctypes.c_void_p),
+        ("gk_vid", ctypes.c_void_p),
+        ("gq_txt", ctypes.c_void_p),
+        ("gk_txt", ctypes.c_void_p),
+        ("shifted", ctypes.c_int),
+        ("wt", ctypes.c_int),
+        ("wh", ctypes.c_int),
+        ("ww", ctypes.c_int),
+        ("threads", ctypes.c_int),
+    ]
+
+
+class OrcBranch(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate",
+        "w_qkv", "w_proj", "b_proj", "norm_q", "norm_k", "w_gate", "w_in", "w_out")]
+
+
+class OrcBlock(ctypes.Structure):
+    _fields_ = [
+        ("dim", ctypes.c_int), ("heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+        ("mlp_hidden", ctypes.c_int), ("eps", ctypes.c_float),
+        ("shared", ctypes.c_int), ("last_layer", ctypes.c_int), ("shifted", ctypes.c_int),
+        ("wt", ctypes.c_int), ("wh", ctypes.c_int), ("ww", ctypes.c_int),
+        ("rope_mode", ctypes.c_int), ("rope_theta", ctypes.c_float), ("qk_norm", ctypes.c_int),
+        ("vid", OrcBranch), ("txt", OrcBranch), ("freqs", ctypes.c_void_p), ("threads", ctypes.c_int),
+    ]
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    lib.orc_bf16.argtypes = [ctypes.c_float]
+    lib.orc_bf16.restype = ctypes.c_float
+    lib.orc_adaptive_window.argtypes = [i, i, i, vp, vp, vp]
+    lib.orc_make_windows.argtypes = [i, i, i, i, i, i, i, vp, i]
+    lib.orc_make_windows.restype = i
+    lib.orc_window_attention.argtypes = [ctypes.POINTER(OrcAttnCfg), i, i, i, i, vp, vp, vp, vp,
+                                         vp, vp, vp, vp, vp]
+    lib.orc_window_attention.restype = i
+    lib.orc_rmsnorm_rows.argtypes = [vp, i, i, ctypes.c_float]
+    lib.orc_ada_input.argtypes = [vp, i, i, vp, vp, vp, i]
+    lib.orc_ada_output_residual.argtypes = [vp, vp, i, i, vp, vp, i]
+    lib.orc_swiglu.argtypes = [vp, vp, ctypes.c_int64]
+    lib.orc_inner_product.argtypes = [vp, i, i, vp, vp, i, vp, i]
+    lib.orc_block_forward.argtypes = [ctypes.POINTER(OrcBlock), vp, i, vp, i, vp, i, i, i, vp, vp]
+    lib.orc_block_forward.restype = i
+    _lib = lib
+    return lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def bf16(x: float) -> float:
+    return load().orc_bf16(ctypes.c_float(x))
+
+
+def adaptive_window(T, H, W):
+    out = (ctypes.c_int * 3)()
+    load().orc_adaptive_window(T, H, W, ctypes.byref(out, 0), ctypes.byref(out, 4), ctypes.byref(out, 8))
+    return tuple(out)
+
+
+def make_windows(T, H, W, shifted=False, wt=0, wh=0, ww=0):
+    lib = load()
+    n = lib.orc_make_windows(T, H, W, int(bool(shifted)), wt, wh, ww, None, 0)
+    arr = (OrcWindow * max(n, 1))()
+    lib.orc_make_windows(T, H, W, int(bool(shifted)), wt, wh, ww, arr, n)
+    return [(w.t0, w.t1, w.h0, w.h1, w.w0, w.w1) for w in arr[:n]]
+
+
+def window_attention(vid_qkv, txt_qkv, T, H, W, *, heads, head_dim=128, eps=1e-5, qk_norm=True,
+                     rope_mode=ROPE_REFERENCE, freqs=None, theta=10000.0, gammas=None,
+                     shifted=False, wt=0, wh=0, ww=0, threads=0, capture=False, video_mask=None):
+    """Returns (vid_out, txt_out) or, with capture=True, also a dict with the
+    q/k/v after the prologue and the pre-rounding outputs in window-sequence order."""
+    lib = load()
+    vid_qkv = _f32(vid_qkv)
+    txt_qkv = _f32(txt_qkv)
+    D = heads * head_dim
+    Lv, Lt = vid_qkv.shape[0], txt_qkv.shape[0]
+    assert vid_qkv.shape[1] == 3 * D and (Lt == 0 or txt_qkv.shape[1] == 3 * D)
+    assert Lv == T * H * W
+    ones = np.ones(head_dim, dtype=np.float32)
+    gq_v, gk_v, gq_t, gk_t = [(_f32(g) if g is not None else ones) for g in (gammas or (None,) * 4)]
+    fr = _f32(freqs) if freqs is not None else np.zeros(21, dtype=np.float32)
+    cfg = OrcAttnCfg(heads, head_dim, eps, int(bool(qk_norm)), rope_mode, _p(fr), theta,
+                     _p(gq_v), _p(gk_v), _p(gq_t), _p(gk_t), int(bool(shifted)), wt, wh, ww, threads)
+    vid_out = np.zeros((Lv, D), dtype=np.float32)
+    txt_out = np.zeros((Lt, D), dtype=np.float32)
+    caps = None
+    cap_ptrs = [None] * 4
+    if capture:
+        wins = make_windows(T, H, W, shifted, wt, wh, ww)
+        total = sum((w[1] - w[0]) * (w[3] - w[2]) * (w[5] - w[4]) + Lt for w in wins)
+        caps = {k: np.zeros((total, D), dtype=np.float32) for k in ("q", "k", "v", "pre")}
+        cap_ptrs = [_p(caps[k]) for k in ("q", "k", "v", "pre")]
+    mask = None
+    if video_mask is not None:
+        mask = np.ascontiguousarray(video_mask, dtype=np.uint8)
+    rc = lib.orc_window_attention(ctypes.byref(cfg), T, H, W, Lt, _p(vid_qkv), _p(txt_qkv),
+                                  _p(vid_out), _p(txt_out), *cap_ptrs, _p(mask))
+    if rc != 0:
+        raise RuntimeError(f"orc_window_attention failed: {rc}")
+    if capture:
+        return vid_out, txt_out, caps
+    return vid_out, txt_out
+
+
+def rmsnorm_rows(x, eps):
+    x = _f32(x).copy()
+    load().orc_rmsnorm_rows(_p(x), x.shape[0], x.shape[1], eps)
+    return x
+
+
+def ada_input(x, emb, shift, scale, slot_base):
+    x = _f32(x).copy()
+    emb, shift, scale = _f32(emb), _f32(shift), _f32(scale)
+    load().orc_ada_input(_p(x), x.shape[0], x.shape[1], _p(emb), _p(shift), _p(scale), slot_base)
+    return x
+
+
+def ada_output_residual(x, residual, emb, gate, slot_base):
+    x = _f32(x).copy()
+    residual, emb, gate = _f32(residual), _f32(emb), _f32(gate)
+    load().orc_ada_output_residual(_p(x), _p(residual), x.shape[0], x.shape[1], _p(emb), _p(gate), slot_base)
+    return x
+
+
+def swiglu(gate, value):
+    g = _f32(gate).copy()
+    v = _f32(value)
+    load().orc_swiglu(_p(g), _p(v), g.size)
+    return g
+
+
+def inner_product(x, weight, bias=None, threads=0):
+    x, weight = _f32(x), _f32(weight)
+    b = None if bias is None else _f32(bias)
+    rows, n_in = x.shape
+    n_out = weight.shape[0]
+    y = np.zeros((rows, n_out), dtype=np.float32)
+    load().orc_inner_product(_p(x), rows, n_in, _p(weight), _p(b), n_out, _p(y), threads)
+    return y
+
+
+BRANCH_FIELDS = ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate",
+                 "w_qkv", "w_proj", "b_proj", "norm_q", "norm_k", "w_gate", "w_in", "w_out")
+
+
+def block_forward(weights, vid, txt, emb, T, H, W, *, dim, heads, head_dim=128, mlp_hidden,
+                  eps=1e-5, shared=False, last_layer=False, shifted=False, wt=0, wh=0, ww=0,
+                  rope_mode=ROPE_REFERENCE, theta=10000.0, qk_norm=True, threads=0):
+    """weights: {"vid": {field: array}, "txt": {...} (unless shared), "freqs": [21]}."""
+    keep = []
+
+    def branch(d):
+        arrs = {k: _f32(d[k]) for k in BRANCH_FIELDS}
+        keep.append(arrs)
+        return OrcBranch(*[_p(arrs[k]) for k in BRANCH_FIELDS])
+
+    vb = branch(weights["vid"])
+    tb = vb if shared else branch(weights["txt"])
+    freqs = _f32(weights["freqs"])
+    blk = OrcBlock(dim, heads, head_dim, mlp_hidden, eps, int(shared), int(last_layer), int(shifted),
+                   wt, wh, ww, rope_mode, theta, int(qk_norm), vb, tb, _p(freqs), threads)
+    vid, txt, emb = _f32(vid), _f32(txt), _f32(emb)
+    vid_out = np.zeros_like(vid)
+    txt_out = np.zeros_like(txt)
+    rc = load().orc_block_forward(ctypes.byref(blk), _p(vid), vid.shape[0], _p(txt), txt.shape[0],
+                                  _p(emb), T, H, W, _p(vid_out), _p(txt_out))
+    if rc != 0:
+        raise RuntimeError(f"orc_block_forward failed: {rc}")
+    return vid_out, txt_out

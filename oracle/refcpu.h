@@ -1,0 +1,158 @@
+/*
+ * refcpu — CPU oracle for the SeedVR2 DiT windowed multimodal attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
+ * SeedVR2DiTBlock fp32 CPU layer (src/layers/seedvr2_dit_block.cpp:58-79,
+ * :643-688, :770-1267 of czwdysj/seedvr2-ncnn-valkan).  It is the checker the
+ * parity tests, the smoke check and the CPU-baseline leg of the benchmark
+ * compare the HIP path against.  Nothing in the product links or calls it.
+ *
+ * Each function cites the reference lines it follows.  Arithmetic follows the
+ * reference op for op: double accumulations where the reference uses double,
+ * float casts at the same points, bf16 round-to-nearest-even at the same
+ * points, window order w -> h -> t, text outputs averaged over windows in
+ * window order.  Build with -ffp-contract=off so no multiply-add is fused
+ * (the reference is built for baseline x86-64, which has no FMA).
+ *
+ * Pinning status (what checks each function beyond its own formula):
+ *   orc_bf16            exhaustive-by-class test against torch's bfloat16 cast
+ *   orc_make_windows    hand-derived known-answer plans, partition invariants,
+ *                       exact-rational brute force over small grids
+ *   orc_window_attention textbook softmax attention in float64 on tiny shapes,
+ *                       S=1 / identical-key / one-hot special cases, RoPE as
+ *                       complex rotation, norm preservation, window-masked
+ *                       global attention formulation
+ *   orc_rmsnorm_rows, orc_ada_input, orc_ada_output_residual, orc_swiglu
+ *                       closed forms in float64 numpy
+ *   orc_inner_product   y = W x + b in float64 (summation order of ncnn's
+ *                       InnerProduct is not available here: parity unpinned
+ *                       for GEMM summation order, values pinned by closed form)
+ *   orc_block_forward   composition of the above; parity unpinned against
+ *                       the reference block itself (no stored golden outputs
+ *                       exist in the reference and ncnn is absent)
+ */
+#ifndef SEEDVR2_REFCPU_H
+#define SEEDVR2_REFCPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_window {
+    int t0, t1, h0, h1, w0, w1;
+} orc_window;
+
+/* RoPE variants. */
+enum {
+    ORC_ROPE_REFERENCE = 0, /* 3 axes x 21 adjacent pairs, window-local positions, text rotated at (l,l,l) */
+    ORC_ROPE_ABSOLUTE = 1,  /* head_dim split 32/48/48 over t/h/w, absolute grid positions, text not rotated */
+    ORC_ROPE_NONE = 2
+};
+
+/* bf16 round-to-nearest-even kept in an fp32 container (seedvr2_dit_block.cpp:68-79). */
+float orc_bf16(float value);
+
+/* Adaptive window size rule (seedvr2_dit_block.cpp:832-838). */
+void orc_adaptive_window(int T, int H, int W, int* wt, int* wh, int* ww);
+
+/* Window plan (seedvr2_dit_block.cpp:827-868).  wt/wh/ww == 0 selects the
+ * reference adaptive size on that axis.  Returns the number of windows, or
+ * -1 if it exceeds cap (out may be NULL with cap 0 to query the count). */
+int orc_make_windows(int T, int H, int W, int shifted, int wt, int wh, int ww,
+                     orc_window* out, int cap);
+
+typedef struct orc_attn_cfg {
+    int heads;
+    int head_dim;
+    float eps;
+    int qk_norm;            /* 1: per-head RMSNorm * gamma on q and k (reference); 0: none */
+    int rope_mode;          /* ORC_ROPE_* */
+    const float* freqs;     /* [21] rope frequencies (reference mode) */
+    float rope_theta;       /* absolute mode */
+    const float* gq_vid;    /* [head_dim] norm_q of the video branch */
+    const float* gk_vid;
+    const float* gq_txt;    /* [head_dim] norm_q of the text branch (vid branch if shared) */
+    const float* gk_txt;
+    int shifted;
+    int wt, wh, ww;         /* 0 = adaptive */
+    int threads;            /* OpenMP threads over heads; <= 0 uses the default */
+} orc_attn_cfg;
+
+/* Windowed joint video+text attention (seedvr2_dit_block.cpp:870-1091).
+ * vid_qkv [Lv, 3D] and txt_qkv [Lt, 3D] rows, q at column h*hd, k at D+h*hd,
+ * v at 2D+h*hd.  Outputs vid_out [Lv, D], txt_out [Lt, D].
+ * Optional captures (NULL to skip), each [sum_w S_w, D] in window-sequence
+ * order (video tokens t->y->x, then text): q/k/v after the prologue, and the
+ * attention output before its bf16 rounding.
+ * video_mask (optional, [nW]): video queries of window w are evaluated only if
+ * video_mask[w] != 0 (text queries always are, since the text output averages
+ * over every window); skipped video rows of vid_out are left untouched.
+ * Returns 0, or -1 on a shape mismatch. */
+int orc_window_attention(const orc_attn_cfg* cfg, int T, int H, int W, int Lt,
+                         const float* vid_qkv, const float* txt_qkv,
+                         float* vid_out, float* txt_out,
+                         float* cap_q, float* cap_k, float* cap_v, float* cap_pre,
+                         const unsigned char* video_mask);
+
+/* Token RMSNorm over the last dim, no gamma (seedvr2_dit_block.cpp:770-782). */
+void orc_rmsnorm_rows(float* x, int rows, int dim, float eps);
+
+/* Ada input modulation (seedvr2_dit_block.cpp:784-805); slot_base 0 (attn) or 3 (mlp). */
+void orc_ada_input(float* x, int rows, int dim, const float* emb, const float* shift,
+                   const float* scale, int slot_base);
+
+/* Gated residual (seedvr2_dit_block.cpp:807-825); gate slot = slot_base + 2. */
+void orc_ada_output_residual(float* x, const float* residual, int rows, int dim,
+                             const float* emb, const float* gate, int slot_base);
+
+/* SwiGLU gate g <- silu(g) * v (seedvr2_dit_block.cpp:58-61, :1093-1112). */
+void orc_swiglu(float* gate, const float* value, int64_t count);
+
+/* ncnn InnerProduct semantics: y[r][o] = b[o] + sum_i W[o][i] * x[r][i],
+ * W row-major [out][in].  Accumulated in double. */
+void orc_inner_product(const float* x, int rows, int in, const float* weight,
+                       const float* bias, int out, float* y, int threads);
+
+typedef struct orc_branch {
+    const float* attn_shift;
+    const float* attn_scale;
+    const float* attn_gate;
+    const float* mlp_shift;
+    const float* mlp_scale;
+    const float* mlp_gate;
+    const float* w_qkv;   /* [3D][D] */
+    const float* w_proj;  /* [D][D] */
+    const float* b_proj;  /* [D] */
+    const float* norm_q;  /* [hd] */
+    const float* norm_k;  /* [hd] */
+    const float* w_gate;  /* [F][D] */
+    const float* w_in;    /* [F][D] */
+    const float* w_out;   /* [D][F] */
+} orc_branch;
+
+typedef struct orc_block {
+    int dim, heads, head_dim, mlp_hidden;
+    float eps;
+    int shared, last_layer, shifted;
+    int wt, wh, ww;
+    int rope_mode;
+    float rope_theta;
+    int qk_norm;
+    orc_branch vid;
+    orc_branch txt;       /* ignored when shared */
+    const float* freqs;   /* [21] */
+    int threads;
+} orc_block;
+
+/* One block forward (seedvr2_dit_block.cpp:1114-1267).  vid [Lv, D], txt [Lt, D],
+ * emb [6D].  Returns 0, -1 on invalid shapes, -100 on allocation failure. */
+int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt,
+                      const float* emb, int T, int H, int W, float* vid_out, float* txt_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

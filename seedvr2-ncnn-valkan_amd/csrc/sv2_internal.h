@@ -1,0 +1,108 @@
+// Internal declarations shared by the host launch layer and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "seedvr2_hip.h"
+
+namespace sv2
+{
+
+// Head dimension the MFMA tiling is written for (SeedVR2-3B: 20 heads x 128).
+constexpr int kHeadDim = 128;
+
+// Most non-empty window intervals one axis may have; the per-axis boundary
+// lists travel to the kernels by value in the kernel arguments.
+constexpr int kMaxAxisIntervals = 48;
+
+// Pairs per RoPE axis slot in the cos/sin table (reference: 21, absolute: 16/24/24).
+constexpr int kRopePairSlots = 24;
+
+// The non-empty intervals of one axis of a window plan, as boundaries:
+// interval i is [b[i], b[i+1]).  They partition [0, extent).
+struct AxisPlan
+{
+    int n;
+    int b[kMaxAxisIntervals + 1];
+};
+
+// A window plan in closed form.  The reference enumerates windows w-outer,
+// h-middle, t-inner and skips empty ones (seedvr2_dit_block.cpp:853-866);
+// an axis interval is empty independently of the other axes, so the kept
+// windows are exactly the product of the per-axis non-empty intervals in that
+// order, and window index wi decodes as it = wi % nt, ih = (wi / nt) % nh,
+// iw = wi / (nt * nh).
+struct PlanArgs
+{
+    AxisPlan t, h, w;
+    int T, H, W;
+    int nwin;
+};
+
+struct WindowBox
+{
+    int t0, t1, h0, h1, w0, w1;
+    int lt, lh, lw;
+    int vlen;    // video tokens in the window
+    int vprefix; // video tokens of all earlier windows (window-sequence offset)
+};
+
+__host__ __device__ inline WindowBox window_box(const PlanArgs& p, int wi)
+{
+    const int it = wi % p.t.n;
+    const int rest = wi / p.t.n;
+    const int ih = rest % p.h.n;
+    const int iw = rest / p.h.n;
+    WindowBox b;
+    b.t0 = p.t.b[it];
+    b.t1 = p.t.b[it + 1];
+    b.h0 = p.h.b[ih];
+    b.h1 = p.h.b[ih + 1];
+    b.w0 = p.w.b[iw];
+    b.w1 = p.w.b[iw + 1];
+    b.lt = b.t1 - b.t0;
+    b.lh = b.h1 - b.h0;
+    b.lw = b.w1 - b.w0;
+    b.vlen = b.lt * b.lh * b.lw;
+    // earlier windows: every full w-column before iw, then the full h-rows
+    // before ih within column iw, then the t-slices before it
+    b.vprefix = b.w0 * p.H * p.T + b.lw * b.h0 * p.T + b.lw * b.lh * b.t0;
+    return b;
+}
+
+// Global video row of local token j (t -> y -> x order) of a window.
+__host__ __device__ inline int window_video_row(const PlanArgs& p, const WindowBox& b, int j,
+                                                int* lt_out, int* ly_out, int* lx_out)
+{
+    const int plane = b.lh * b.lw;
+    const int t = j / plane;
+    const int rem = j - t * plane;
+    const int y = rem / b.lw;
+    const int x = rem - y * b.lw;
+    *lt_out = t;
+    *ly_out = y;
+    *lx_out = x;
+    return ((b.t0 + t) * p.H + (b.h0 + y)) * p.W + (b.w0 + x);
+}
+
+// bf16 round-to-nearest-even on the raw bits, kept in an fp32 container
+// (the arithmetic of seedvr2_dit_block.cpp:68-79).
+__host__ __device__ inline float bf16_round(float value)
+{
+    uint32_t bits = __builtin_bit_cast(uint32_t, value);
+    bits += 0x7fffu + ((bits >> 16) & 1u);
+    bits &= 0xffff0000u;
+    return __builtin_bit_cast(float, bits);
+}
+
+// Thread-local error message plumbing for the C ABI.
+int set_error(int code, const std::string& message);
+int hip_error(hipError_t err, const char* what);
+
+// Builds the closed-form plan; returns SV2_OK or an error code.
+int build_plan(const sv2_window_rule& rule, PlanArgs* plan);
+
+} // namespace sv2

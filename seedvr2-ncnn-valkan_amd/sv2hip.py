@@ -1,0 +1,277 @@
+"""ctypes binding of libseedvr2_hip.so (the C ABI in include/seedvr2_hip.h).
+
+Thin plumbing for tests, the smoke check and the benchmark: device memory and
+streams come from PyTorch, every computation runs in the HIP library.  Loading
+fails loudly when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libseedvr2_hip.so"
+
+SV2_OK = 0
+SV2_EINVAL = -1
+SV2_EUNSUPPORTED = -2
+SV2_EDEVICE = -100
+
+F32, F16, BF16 = 0, 1, 2
+ROPE_REFERENCE, ROPE_ABSOLUTE, ROPE_NONE = 0, 1, 2
+
+# Exported symbols declared in include/seedvr2_hip.h.
+EXPORTS = [
+    "sv2_window_plan",
+    "sv2_window_index_map",
+    "sv2_rope_table_floats",
+    "sv2_rope_table_build",
+    "sv2_rope_positions_needed",
+    "sv2_window_attention_workspace",
+    "sv2_window_attention",
+    "sv2_qk_prologue",
+    "sv2_rmsnorm_ada",
+    "sv2_ada_residual",
+    "sv2_swiglu",
+    "sv2_last_error",
+    "sv2_version",
+]
+
+
+class WindowRule(ctypes.Structure):
+    _fields_ = [
+        ("frames", ctypes.c_int),
+        ("height", ctypes.c_int),
+        ("width", ctypes.c_int),
+        ("shifted", ctypes.c_int),
+        ("wt", ctypes.c_int),
+        ("wh", ctypes.c_int),
+        ("ww", ctypes.c_int),
+    ]
+
+
+class Window(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("t0", "t1", "h0", "h1", "w0", "w1")]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("rule", WindowRule),
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("text_len", ctypes.c_int),
+        ("eps", ctypes.c_float),
+        ("qk_norm", ctypes.c_int),
+        ("rope_mode", ctypes.c_int),
+        ("rope_table", ctypes.c_void_p),
+        ("rope_npos", ctypes.c_int),
+        ("vid_qkv", ctypes.c_void_p),
+        ("txt_qkv", ctypes.c_void_p),
+        ("qkv_dtype", ctypes.c_int),
+        ("gamma_q_vid", ctypes.c_void_p),
+        ("gamma_k_vid", ctypes.c_void_p),
+        ("gamma_q_txt", ctypes.c_void_p),
+        ("gamma_k_txt", ctypes.c_void_p),
+        ("vid_out", ctypes.c_void_p),
+        ("txt_out", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("debug_pre", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads the HIP library; raises if it is missing (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+            "(the HIP path has no CPU fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, ip, i = ctypes.c_void_p, ctypes.c_int, ctypes.c_int
+    lib.sv2_window_plan.argtypes = [ctypes.POINTER(WindowRule), ctypes.POINTER(Window), i]
+    lib.sv2_window_plan.restype = i
+    lib.sv2_window_index_map.argtypes = [ctypes.POINTER(WindowRule), vp, vp]
+    lib.sv2_window_index_map.restype = i
+    lib.sv2_rope_table_floats.argtypes = [i]
+    lib.sv2_rope_table_floats.restype = ctypes.c_size_t
+    lib.sv2_rope_table_build.argtypes = [i, vp, ctypes.c_float, i, vp]
+    lib.sv2_rope_table_build.restype = i
+    lib.sv2_rope_positions_needed.argtypes = [ctypes.POINTER(WindowRule), i, i]
+    lib.sv2_rope_positions_needed.restype = i
+    lib.sv2_window_attention_workspace.argtypes = [ctypes.POINTER(AttnArgs)]
+    lib.sv2_window_attention_workspace.restype = ctypes.c_int64
+    lib.sv2_window_attention.argtypes = [ctypes.POINTER(AttnArgs), vp]
+    lib.sv2_window_attention.restype = i
+    lib.sv2_qk_prologue.argtypes = [ctypes.POINTER(AttnArgs), vp, vp, vp, vp]
+    lib.sv2_qk_prologue.restype = i
+    lib.sv2_rmsnorm_ada.argtypes = [vp, vp, i, i, i, ctypes.c_float, vp, vp, vp, i, i, vp]
+    lib.sv2_rmsnorm_ada.restype = i
+    lib.sv2_ada_residual.argtypes = [vp, vp, i, i, i, vp, vp, i, i, vp]
+    lib.sv2_ada_residual.restype = i
+    lib.sv2_swiglu.argtypes = [vp, vp, i, ctypes.c_int64, vp]
+    lib.sv2_swiglu.restype = i
+    lib.sv2_last_error.argtypes = []
+    lib.sv2_last_error.restype = ctypes.c_char_p
+    lib.sv2_version.argtypes = []
+    lib.sv2_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+class Sv2Error(RuntimeError):
+    def __init__(self, code: int, what: str):
+        msg = load().sv2_last_error().decode()
+        super().__init__(f"{what} failed ({code}): {msg}")
+        self.code = code
+
+
+def check(code: int, what: str) -> int:
+    if code < 0:
+        raise Sv2Error(code, what)
+    return code
+
+
+def rule(frames, height, width, shifted=False, wt=0, wh=0, ww=0) -> WindowRule:
+    return WindowRule(frames, height, width, int(bool(shifted)), wt, wh, ww)
+
+
+def window_plan(r: WindowRule) -> list[tuple[int, int, int, int, int, int]]:
+    lib = load()
+    n = check(lib.sv2_window_plan(ctypes.byref(r), None, 0), "sv2_window_plan")
+    arr = (Window * max(n, 1))()
+    check(lib.sv2_window_plan(ctypes.byref(r), arr, n), "sv2_window_plan")
+    return [(w.t0, w.t1, w.h0, w.h1, w.w0, w.w1) for w in arr[:n]]
+
+
+def rope_positions_needed(r: WindowRule, text_len: int, mode: int) -> int:
+    return check(load().sv2_rope_positions_needed(ctypes.byref(r), text_len, mode),
+                 "sv2_rope_positions_needed")
+
+
+def rope_table(mode: int, freqs, theta: float, npos: int) -> np.ndarray:
+    lib = load()
+    n = lib.sv2_rope_table_floats(npos)
+    out = np.zeros(n, dtype=np.float32)
+    fr = None
+    if freqs is not None:
+        fr = np.ascontiguousarray(freqs, dtype=np.float32)
+    check(lib.sv2_rope_table_build(mode, fr.ctypes.data if fr is not None else None,
+                                   ctypes.c_float(theta), npos, out.ctypes.data),
+          "sv2_rope_table_build")
+    return out
+
+
+def torch_dtype_code(t) -> int:
+    import torch
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[t.dtype]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+class WindowAttention:
+    """Owns the device-side constants (rope table, workspace) of one attention
+    configuration and launches sv2_window_attention on torch tensors."""
+
+    def __init__(self, r: WindowRule, heads: int, text_len: int, *, eps=1e-5, qk_norm=True,
+                 rope_mode=ROPE_REFERENCE, freqs=None, theta=10000.0, device="cuda"):
+        import torch
+        self.rule = r
+        self.heads = heads
+        self.text_len = text_len
+        self.eps = eps
+        self.qk_norm = qk_norm
+        self.rope_mode = rope_mode
+        self.npos = rope_positions_needed(r, text_len, rope_mode)
+        if rope_mode != ROPE_NONE:
+            tab = rope_table(rope_mode, freqs, theta, self.npos)
+            self.rope = torch.from_numpy(tab).to(device)
+        else:
+            self.rope = None
+        self.plan = window_plan(r)
+        self.device = device
+        self.workspace = None
+
+    def args(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None) -> AttnArgs:
+        gq_v, gk_v, gq_t, gk_t = gammas if gammas is not None else (None,) * 4
+        a = AttnArgs()
+        a.rule = self.rule
+        a.heads = self.heads
+        a.head_dim = 128
+        a.text_len = self.text_len
+        a.eps = self.eps
+        a.qk_norm = int(bool(self.qk_norm))
+        a.rope_mode = self.rope_mode
+        a.rope_table = None if self.rope is None else self.rope.data_ptr()
+        a.rope_npos = self.npos
+        a.vid_qkv = vid_qkv.data_ptr()
+        a.txt_qkv = None if txt_qkv is None else txt_qkv.data_ptr()
+        a.qkv_dtype = torch_dtype_code(vid_qkv)
+        a.gamma_q_vid = None if gq_v is None else gq_v.data_ptr()
+        a.gamma_k_vid = None if gk_v is None else gk_v.data_ptr()
+        a.gamma_q_txt = None if gq_t is None else gq_t.data_ptr()
+        a.gamma_k_txt = None if gk_t is None else gk_t.data_ptr()
+        a.vid_out = vid_out.data_ptr()
+        a.txt_out = None if txt_out is None else txt_out.data_ptr()
+        a.out_dtype = torch_dtype_code(vid_out)
+        a.debug_pre = None if debug_pre is None else debug_pre.data_ptr()
+        return a
+
+    def workspace_bytes(self, a: AttnArgs) -> int:
+        return check(load().sv2_window_attention_workspace(ctypes.byref(a)),
+                     "sv2_window_attention_workspace")
+
+    def __call__(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
+        import torch
+        a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
+        need = self.workspace_bytes(a)
+        if need > 0 and (self.workspace is None or self.workspace.numel() < need):
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=vid_qkv.device)
+        a.workspace = None if need == 0 else self.workspace.data_ptr()
+        a.workspace_bytes = need
+        check(load().sv2_window_attention(ctypes.byref(a), _stream(stream)), "sv2_window_attention")
+
+    def prologue(self, vid_qkv, txt_qkv, gammas, q_out, k_out, v_out, stream=None):
+        a = self.args(vid_qkv, txt_qkv, gammas, q_out, None)
+        check(load().sv2_qk_prologue(ctypes.byref(a), _ptr(q_out), _ptr(k_out), _ptr(v_out),
+                                     _stream(stream)), "sv2_qk_prologue")
+
+
+def window_index_map(r: WindowRule, out, stream=None):
+    check(load().sv2_window_index_map(ctypes.byref(r), _ptr(out), _stream(stream)),
+          "sv2_window_index_map")
+
+
+def rmsnorm_ada(x, y, eps, emb=None, shift=None, scale=None, slot_base=0, has_ada=True, stream=None):
+    rows, dim = x.shape
+    check(load().sv2_rmsnorm_ada(_ptr(x), _ptr(y), torch_dtype_code(x), rows, dim, ctypes.c_float(eps),
+                                 _ptr(emb), _ptr(shift), _ptr(scale), slot_base, int(bool(has_ada)),
+                                 _stream(stream)), "sv2_rmsnorm_ada")
+
+
+def ada_residual(x, residual, emb=None, gate=None, slot_base=0, mode=0, stream=None):
+    rows, dim = x.shape
+    check(load().sv2_ada_residual(_ptr(x), _ptr(residual), torch_dtype_code(x), rows, dim, _ptr(emb),
+                                  _ptr(gate), slot_base, mode, _stream(stream)), "sv2_ada_residual")
+
+
+def swiglu(gate, value, stream=None):
+    check(load().sv2_swiglu(_ptr(gate), _ptr(value), torch_dtype_code(gate), gate.numel(),
+                            _stream(stream)), "sv2_swiglu")

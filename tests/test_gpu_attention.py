@@ -1,0 +1,133 @@
+"""GPU parity of the windowed joint attention (sv2_window_attention) against
+the CPU oracle on identical seeded inputs.
+
+Cases: the single-layer shapes of the benchmark configurations (grid 2x16x30,
+20 heads, 58 text tokens, 2x8x10 windows, unshifted and shifted), the
+reference's adaptive windows (no explicit size), the 720p grid 6x45x80 with
+2x9x16 windows (video outputs checked on a sample of windows, text outputs on
+all of them), the four small cases of the reference's own CPU-vs-Vulkan block
+test (tests/dit_block_vulkan_runner.cpp:213-218) at the attention level, and
+edge cases (one token, no text tokens).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch  # noqa: F401  (first import is slow on a fresh box; keep it out of test timeouts)
+
+from attn_case import run_attention_case as _case
+from parity import reference_freqs
+
+pytestmark = pytest.mark.gpu
+
+L_TXT = 58  # embeddings/default_pos_emb.bin header [58, 5120]
+
+
+def test_single_layer_2x16x30_unshifted_no_norm_no_rope(hip, orc, device):
+    # the CPU-reference layer shape: windows 2x8x10 (6), no RoPE, no QK-norm
+    _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=20, wt=2, wh=8, ww=10,
+          qk_norm=False, rope_mode=2, in_dtype="f32", out_dtype="f32", seed=1)
+
+
+def test_single_layer_2x16x30_fp16_shifted_norm_rope(hip, orc, device):
+    # fp16 layer with QK-norm and RoPE, shifted (0,4,5) ragged windows (12)
+    _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=20, shifted=True, wt=2, wh=8, ww=10,
+          qk_norm=True, rope_mode=0, in_dtype="f16", out_dtype="f16", seed=2)
+
+
+def test_single_layer_2x16x30_absolute_rope(hip, orc, device):
+    _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=20, shifted=True, wt=2, wh=8, ww=10,
+          qk_norm=True, rope_mode=1, in_dtype="f16", out_dtype="bf16", seed=3)
+
+
+@pytest.mark.parametrize("shifted", [False, True])
+def test_reference_adaptive_windows(hip, orc, device, shifted):
+    # no explicit window size: the reference's adaptive rule (1x15x28 here)
+    _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=4, shifted=shifted,
+          in_dtype="bf16", out_dtype="f32", seed=4 + shifted)
+
+
+@pytest.mark.parametrize("shifted", [False, True])
+def test_720p_grid_sampled_windows(hip, orc, device, shifted):
+    # 6x45x80 with 2x9x16 windows; video outputs on a sample of windows,
+    # text outputs (which average over every window) in full
+    n = len(orc.make_windows(6, 45, 80, shifted, 2, 9, 16))
+    sample = sorted({0, 1, n // 3, n // 2, n - 2, n - 1})
+    _case(hip, orc, device, T=6, H=45, W=80, Lt=L_TXT, heads=20, shifted=shifted, wt=2, wh=9, ww=16,
+          in_dtype="f16", out_dtype="f16", seed=10 + shifted, video_windows=sample)
+
+
+@pytest.mark.parametrize("case", [
+    # tests/dit_block_vulkan_runner.cpp:213-218 at the attention level
+    dict(T=2, H=2, W=2, Lt=3, heads=1, shifted=False),
+    dict(T=2, H=2, W=2, Lt=3, heads=1, shifted=True),
+    dict(T=1, H=1, W=1, Lt=2, heads=1, shifted=False),
+    dict(T=3, H=2, W=2, Lt=4, heads=2, shifted=False),
+])
+def test_reference_runner_shapes(hip, orc, device, case):
+    _case(hip, orc, device, **case, in_dtype="f32", out_dtype="f32", seed=20)
+
+
+def test_no_text_tokens(hip, orc, device):
+    _case(hip, orc, device, T=2, H=5, W=7, Lt=0, heads=2, shifted=True, wt=1, wh=2, ww=3,
+          in_dtype="f16", out_dtype="f32", seed=30)
+
+
+def test_long_text_many_key_blocks(hip, orc, device):
+    # S spans several 64-key blocks and 128-query blocks with ragged tails
+    _case(hip, orc, device, T=3, H=7, W=9, Lt=150, heads=3, shifted=True, wt=2, wh=4, ww=5,
+          in_dtype="f16", out_dtype="f32", seed=31)
+
+
+def test_index_map_bitexact(hip, orc, device):
+    import torch
+    for (T, H, W, sh, wt, wh, ww) in [(2, 16, 30, False, 2, 8, 10), (2, 16, 30, True, 2, 8, 10),
+                                      (6, 45, 80, True, 2, 9, 16), (6, 45, 80, False, 0, 0, 0),
+                                      (2, 16, 30, True, 0, 0, 0), (5, 7, 3, True, 2, 2, 2)]:
+        print(f"[index map] {T}x{H}x{W} shifted={sh} win=({wt},{wh},{ww})", flush=True)
+        out = torch.full((T * H * W,), -1, dtype=torch.int32, device=device)
+        hip.window_index_map(hip.rule(T, H, W, sh, wt, wh, ww), out)
+        torch.cuda.synchronize()
+        ref = [((t * H + y) * W + x) for (t0, t1, h0, h1, w0, w1) in orc.make_windows(T, H, W, sh, wt, wh, ww)
+               for t in range(t0, t1) for y in range(h0, h1) for x in range(w0, w1)]
+        assert np.array_equal(out.cpu().numpy(), np.array(ref, dtype=np.int32))
+
+
+@pytest.mark.parametrize("rope_mode,in_dtype", [(0, "f16"), (1, "f32"), (2, "bf16")])
+def test_prologue_matches_oracle_bits(hip, orc, device, rope_mode, in_dtype):
+    """q/k/v after norm, rotation and bf16 rounding: the RoPE table holds the
+    host C library's cosf/sinf, multiplies and adds are unfused, so the device
+    values equal the oracle's bit for bit except where a double sum of squares
+    summed in another order rounds to a different float (rare)."""
+    import torch
+    T, H, W, Lt, heads = 2, 16, 30, L_TXT, 4
+    print(f"[prologue] rope={rope_mode} in={in_dtype}", flush=True)
+    rng = np.random.default_rng(40 + rope_mode)
+    D = heads * 128
+    vid = rng.standard_normal((T * H * W, 3 * D), dtype=np.float32) * 3
+    txt = rng.standard_normal((Lt, 3 * D), dtype=np.float32) * 3
+    tdt = {"f16": torch.float16, "f32": torch.float32, "bf16": torch.bfloat16}[in_dtype]
+    vid = torch.from_numpy(vid).to(tdt).float().numpy()
+    txt = torch.from_numpy(txt).to(tdt).float().numpy()
+    gam = rng.uniform(0.5, 1.5, (4, 128)).astype(np.float32)
+    freqs = reference_freqs()
+    _, _, caps = orc.window_attention(vid, txt, T, H, W, heads=heads, rope_mode=rope_mode, freqs=freqs,
+                                      gammas=list(gam), shifted=True, wt=2, wh=8, ww=10, capture=True)
+    attn = hip.WindowAttention(hip.rule(T, H, W, True, 2, 8, 10), heads, Lt, rope_mode=rope_mode,
+                               freqs=freqs, device=device)
+    outs = [torch.full(caps["q"].shape, float("nan"), device=device) for _ in range(3)]
+    attn.prologue(torch.from_numpy(vid).to(device, tdt), torch.from_numpy(txt).to(device, tdt),
+                  [torch.from_numpy(g).to(device) for g in gam], *outs)
+    torch.cuda.synchronize()
+    for name, o in zip("qkv", outs):
+        g = o.cpu().numpy()
+        r = caps[name]
+        differ = g.view(np.uint32) != r.view(np.uint32)
+        frac = differ.mean()
+        print(f"  {name}: {int(differ.sum())} of {g.size} differ", flush=True)
+        assert np.isfinite(g).all()
+        assert frac <= 1e-5, f"{name}: {frac:.2e} of the elements differ"
+        if differ.any():
+            d = np.abs(g[differ].astype(np.float64) - r[differ])
+            ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(g[differ]), np.abs(r[differ])))[1] - 8)
+            assert (d <= ulp * 1.000001).all()
