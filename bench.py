@@ -1,0 +1,214 @@
+"""Benchmark of the windowed multimodal attention path on one MI355X.
+
+Workload: the SeedVR2-3B DiT windowed MM-attention at 720p x 21 frames — latent
+grid 6x45x80 (21600 video tokens), windows 2x9x16, 20 heads x 128 dims, 58
+text tokens attended jointly by every window, fp16 activations N(0,1),
+QK-RMSNorm (gamma ~ U(0.5, 1.5)) + RoPE (the reference's mmrope3d).  A step
+is one unshifted layer (75 windows) followed by one shifted layer (144 ragged
+windows), as consecutive DiT blocks alternate them.  Inputs are resident in
+HBM before timing starts.
+
+Prints one JSON line: window-attention TFLOPS of the step (algorithmic flops
+sum_w 4 * S_w^2 * 128 * 20 / time), the roofline of the attention launches
+(HBM-bound: algorithmic bytes = one read of q/k/v and one write of the
+outputs), and the CPU oracle timed on a bounded sample on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "seedvr2-ncnn-valkan_amd", REPO / "tests", REPO / "oracle"):
+    sys.path.insert(0, str(p))
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+T, H, W, L_TXT, HEADS, HD = 6, 45, 80, 58, 20, 128
+WIN = (2, 9, 16)
+
+
+def plan_stats(shifted: bool):
+    import oracle
+    wins = oracle.make_windows(T, H, W, shifted, *WIN)
+    sizes = [(w[1] - w[0]) * (w[3] - w[2]) * (w[5] - w[4]) for w in wins]
+    flops = sum(4.0 * (v + L_TXT) ** 2 * HD * HEADS for v in sizes)
+    return wins, sizes, flops
+
+
+def algorithmic_bytes(elem=2):
+    tokens = T * H * W + L_TXT
+    return tokens * 3 * HEADS * HD * elem + tokens * HEADS * HD * elem
+
+
+def cpu_baseline(target_s: float = 15.0):
+    """The CPU oracle on the shifted 720p plan: video queries of a sample of
+    windows plus the text queries of every window (the text output averages
+    over all windows).  Returns TFLOPS of the work actually done."""
+    import oracle
+    from parity import reference_freqs
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, 16, HEADS))
+    wins, sizes, _ = plan_stats(True)
+    rng = np.random.default_rng(7)
+    D = HEADS * HD
+    vid = rng.standard_normal((T * H * W, 3 * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    txt = rng.standard_normal((L_TXT, 3 * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    gam = list(rng.uniform(0.5, 1.5, (4, 128)).astype(np.float32))
+    freqs = reference_freqs()
+
+    def run(k):
+        mask = np.zeros(len(wins), np.uint8)
+        mask[np.linspace(0, len(wins) - 1, k).astype(int)] = 1
+        work = 0.0
+        for wi, v in enumerate(sizes):
+            s = v + L_TXT
+            queries = (v if mask[wi] else 0) + L_TXT
+            work += 4.0 * queries * s * HD * HEADS
+        t0 = time.perf_counter()
+        oracle.window_attention(vid, txt, T, H, W, heads=HEADS, freqs=freqs, gammas=gam, shifted=True,
+                                wt=WIN[0], wh=WIN[1], ww=WIN[2], threads=threads, video_mask=mask)
+        return time.perf_counter() - t0, work, int(mask.sum())
+
+    # two-point fit: a fixed cost (text queries of every window) plus a cost
+    # per window whose video queries are evaluated
+    t_a, _, _ = run(4)
+    t_b, _, _ = run(12)
+    per_window = max((t_b - t_a) / 8.0, 1e-4)
+    fixed = max(t_a - 4 * per_window, 0.0)
+    k = int(min(len(wins), max(12, (target_s - fixed) / per_window)))
+    dt, work, k = run(k)
+    return {
+        "value": work / dt / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle (C restatement of the reference CPU layer, OpenMP over heads) on the "
+                   f"shifted 720p plan: video queries of {k} of {len(wins)} windows + text queries of "
+                   f"every window, 20 heads; {work / 1e9:.1f} GFLOP in {dt:.1f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+
+    import torch
+    import sv2hip
+    from parity import reference_freqs
+
+    dev = torch.device("cuda:0")
+    sv2hip.load()
+    D = HEADS * HD
+    rng = np.random.default_rng(0)
+    vid = torch.from_numpy(rng.standard_normal((T * H * W, 3 * D), dtype=np.float32)).to(dev, torch.float16)
+    txt = torch.from_numpy(rng.standard_normal((L_TXT, 3 * D), dtype=np.float32)).to(dev, torch.float16)
+    gam = [torch.from_numpy(g).to(dev) for g in rng.uniform(0.5, 1.5, (4, 128)).astype(np.float32)]
+    freqs = reference_freqs()
+    layers = []
+    for shifted in (False, True):
+        attn = sv2hip.WindowAttention(sv2hip.rule(T, H, W, shifted, *WIN), HEADS, L_TXT, freqs=freqs,
+                                      device=dev)
+        _, _, flops = plan_stats(shifted)
+        layers.append((shifted, attn, flops))
+    out_v = torch.empty((T * H * W, D), dtype=torch.float16, device=dev)
+    out_t = torch.empty((L_TXT, D), dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(events=None):
+        for i, (_, attn, _) in enumerate(layers):
+            if events is not None:
+                events[i][0].record(stream)
+            attn(vid, txt, gam, out_v, out_t, stream=stream)
+            if events is not None:
+                events[i][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in layers] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(ev[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_layer_ms = [float(np.mean([ev[k][i][0].elapsed_time(ev[k][i][1]) for k in range(args.steps)]))
+                    for i in range(len(layers))]
+    flops_step = sum(f for _, _, f in layers)
+    ms_step = wall * 1e3 / args.steps
+    tflops = flops_step / (ms_step * 1e-3) / 1e12
+    B = algorithmic_bytes()
+    variants = {}
+    for (shifted, _, flops), ms in zip(layers, per_layer_ms):
+        t = ms * 1e-3
+        variants["shifted" if shifted else "unshifted"] = {
+            "ms": round(ms, 4),
+            "tflops": round(flops / t / 1e12, 2),
+            "mfma_util": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "hbm_gbs": round(B / t / 1e9, 1),
+            "hbm_util": round(B / t / 1e9 / PEAK_HBM_GBS, 4),
+            "roofline_frac": round(max(flops / (PEAK_FP16_TFLOPS * 1e12), B / (PEAK_HBM_GBS * 1e9)) / t, 4),
+        }
+    t_launch = float(np.mean(per_layer_ms)) * 1e-3
+    achieved = B / t_launch / 1e9
+    traffic = None
+    tf = REPO / "profiles" / "window_attention_720p_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    result = {
+        "metric": "window-attn TFLOPS & % fp16 MFMA peak; DiT step ms @720p×21f, 1 GPU",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("windowed MM-attention 720p x 21f: grid 6x45x80 (21600 video tokens), windows "
+                         "2x9x16, step = unshifted layer (75 windows) + shifted layer (144 ragged windows), "
+                         "20 heads x 128, 58 joint text tokens, fp16 N(0,1) q/k/v, QK-RMSNorm + RoPE "
+                         "(reference mmrope3d)"),
+            "mfma": "bf16 QK^T (exact bf16 q/k), f16 PV, f32 accumulate",
+            "mfma_util": round(tflops / PEAK_FP16_TFLOPS, 4),
+            "variants": variants,
+            "dit_step_ms": None,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -2,23 +2,32 @@
 //
 // Replaces SeedVR2DiTBlock::attention (seedvr2_dit_block.cpp:870-1091) and the
 // reference's per-window qkv_prepare / attention / zero_buffer / window_sum
-// shader chain (:192-330, :339-457, :541-572) with one fused kernel plus a
-// small text reduction:
+// shader chain (:192-330, :339-457, :541-572):
 //
-//   * no materialised window copies: every query and key row is located by
-//     index arithmetic on the closed-form window plan and read straight from
-//     the [tokens, 3*D] qkv rows;
-//   * the per-head RMSNorm * gamma, the RoPE rotation and the bf16 rounding of
-//     q and k (and the bf16 rounding of v) run in registers while a tile is
-//     staged into LDS;
-//   * S^T = K Q^T on bf16 MFMA (q, k are bf16 values, so the operands are
-//     exact), online softmax in fp32 with one cross-lane exchange per row,
-//     O^T += V^T P^T on fp16 MFMA with fp32 accumulation;
-//   * ragged windows are handled by masking keys and padding query rows, never
-//     by padding the tensors;
-//   * video outputs are written once (the windows partition the grid); text
-//     outputs go to per-window bf16 partials which a second kernel sums in
-//     window order and scales by 1/nW, exactly as the reference does.
+//   text_prepare_kernel   the q/k prologue of the L_txt text tokens, once per
+//                         layer (their RoPE positions (l, l, l) do not depend
+//                         on the window), bf16 q/k and transposed fp16 v into
+//                         the workspace;
+//   window_attention_kernel
+//                         one 8-wave workgroup per (window, head) and up to
+//                         256 query rows (larger windows split evenly): every video row of the window is
+//                         located through a per-window row table built in LDS
+//                         from the closed-form plan (no materialised window
+//                         copies), its q/k RMSNorm * gamma, RoPE and bf16
+//                         rounding run in registers (RoPE cos/sin and gammas
+//                         staged in LDS per window), K and V^T tiles of 64
+//                         keys are double-buffered in LDS and three tiles'
+//                         global loads are in flight in registers while a
+//                         tile is consumed;  S^T = K Q^T on bf16 MFMA (exact operands),
+//                         online softmax in fp32 with lazy rescaling,
+//                         O^T += V^T P^T on fp16 MFMA;
+//                         ragged windows are handled by masking keys and
+//                         padding query rows; video outputs are written once
+//                         (the windows partition the grid), text outputs to
+//                         per-window bf16 partials;
+//   text_window_reduce_kernel
+//                         text outputs: partials summed in window order, times
+//                         1/nW, as the reference accumulates them.
 #include "sv2_internal.h"
 
 #include <algorithm>
@@ -32,62 +41,103 @@ namespace
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 
-constexpr int kBlockM = 128;   // query rows per workgroup (4 waves x 32)
-constexpr int kBlockN = 64;    // keys per iteration
-constexpr int kThreads = 256;
-constexpr int kQkStride = 136; // halfs per LDS row of the q and k tiles (128 + 8 pad)
-constexpr int kVtStride = 64;  // halfs per LDS row of the transposed v tile (swizzled)
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;   // 512
+constexpr int kRowsPerGroup = kWaves * 32; // query rows per workgroup
+constexpr int kBlockN = 64;             // keys per tile (two 32x32 S^T subtiles)
+constexpr int kKStride = 136;           // halfs per LDS row of the key tile (128 + 8 pad)
+constexpr int kVtStride = 64;           // halfs per LDS row of the transposed value tile (swizzled)
+constexpr int kTextPad = 64;            // text rows of the prepared workspace are padded to this
+constexpr int kMaxVideoRows = 4096;     // video tokens per window the row table holds
+constexpr int kPrepRows = 16;           // text rows per text_prepare workgroup
+constexpr int kMaxRopeRows = 160;       // RoPE rows (t + y + x positions) of one window staged in LDS
+constexpr float kRescaleLog2 = 8.f;     // O is rescaled only when a row max grows by more than 2^8
 constexpr float kLog2e = 1.4426950408889634f;
+// s_waitcnt immediate for vmcnt(0) with expcnt / lgkmcnt left unconstrained
+// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
+constexpr int kWaitVmcnt0 = 0x0F70;
 
-// Element types of the qkv input and of the outputs.
+// ---------------------------------------------------------------- element types
+
 struct F32
 {
-    using storage = float;
+    static constexpr int kVec = 2; // uint4 per 8 elements
 };
 struct F16
 {
-    using storage = _Float16;
+    static constexpr int kVec = 1;
 };
 struct BF16
 {
-    using storage = uint16_t;
+    static constexpr int kVec = 1;
 };
 
 template <typename T>
-__device__ inline void load8(const void* base, long long offset, float x[8]);
+__device__ inline void load_raw8(const void* base, long long offset, uint4 (&r)[T::kVec])
+{
+    if constexpr (T::kVec == 2)
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + offset);
+        r[0] = src[0];
+        r[1] = src[1];
+    }
+    else
+    {
+        r[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + offset);
+    }
+}
+
+template <typename T>
+__device__ inline void zero_raw8(uint4 (&r)[T::kVec])
+{
+#pragma unroll
+    for (int i = 0; i < T::kVec; i++)
+        r[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <typename T>
+__device__ inline void raw8_to_float(const uint4 (&r)[T::kVec], float x[8]);
 
 template <>
-__device__ inline void load8<F32>(const void* base, long long offset, float x[8])
+__device__ inline void raw8_to_float<F32>(const uint4 (&r)[2], float x[8])
 {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + offset);
-    const float4 a = p[0];
-    const float4 b = p[1];
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    const uint32_t w[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        x[e] = __builtin_bit_cast(float, w[e]);
 }
 
 template <>
-__device__ inline void load8<F16>(const void* base, long long offset, float x[8])
+__device__ inline void raw8_to_float<F16>(const uint4 (&r)[1], float x[8])
 {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(base) + offset);
+    const f16x8 v = __builtin_bit_cast(f16x8, r[0]);
 #pragma unroll
     for (int e = 0; e < 8; e++)
         x[e] = static_cast<float>(v[e]);
 }
 
 template <>
-__device__ inline void load8<BF16>(const void* base, long long offset, float x[8])
+__device__ inline void raw8_to_float<BF16>(const uint4 (&r)[1], float x[8])
 {
-    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + offset);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t w[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
 #pragma unroll
     for (int e = 0; e < 4; e++)
     {
         x[2 * e] = __builtin_bit_cast(float, w[e] << 16);
         x[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
     }
+}
+
+template <typename T>
+__device__ inline void load8(const void* base, long long offset, float x[8])
+{
+    uint4 r[T::kVec];
+    load_raw8<T>(base, offset, r);
+    raw8_to_float<T>(r, x);
 }
 
 template <typename T>
@@ -102,7 +152,6 @@ __device__ inline void store4<F32>(void* base, long long offset, const float v[4
 template <>
 __device__ inline void store4<F16>(void* base, long long offset, const float v[4])
 {
-    typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
     f16x4 h;
     h[0] = static_cast<_Float16>(v[0]);
     h[1] = static_cast<_Float16>(v[1]);
@@ -111,8 +160,8 @@ __device__ inline void store4<F16>(void* base, long long offset, const float v[4
     *reinterpret_cast<f16x4*>(static_cast<_Float16*>(base) + offset) = h;
 }
 
-// bf16 outputs, rounded to nearest even (identity on attention outputs, which
-// are bf16 values already; the text averages are not).
+// bf16 rounded to nearest even (identity on attention outputs, which are
+// bf16 values already; the text averages are not).
 template <>
 __device__ inline void store4<BF16>(void* base, long long offset, const float v[4])
 {
@@ -126,6 +175,45 @@ __device__ inline void store4<BF16>(void* base, long long offset, const float v[
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + offset) = packed;
 }
 
+// 8 floats -> 8 bf16 (round to nearest even, v_cvt_pk_bf16_f32).  For finite
+// values this is the reference's rounding (seedvr2_dit_block.cpp:68-79).
+__device__ inline uint4 to_bf16x8(const float x[8])
+{
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        v[e] = static_cast<__bf16>(x[e]);
+    return __builtin_bit_cast(uint4, v);
+}
+
+template <typename T>
+__device__ inline void store2(void* base, long long offset, float a, float b);
+
+template <>
+__device__ inline void store2<F32>(void* base, long long offset, float a, float b)
+{
+    *reinterpret_cast<float2*>(static_cast<float*>(base) + offset) = make_float2(a, b);
+}
+
+template <>
+__device__ inline void store2<F16>(void* base, long long offset, float a, float b)
+{
+    f16x2 h;
+    h[0] = static_cast<_Float16>(a);
+    h[1] = static_cast<_Float16>(b);
+    *reinterpret_cast<f16x2*>(static_cast<_Float16*>(base) + offset) = h;
+}
+
+template <>
+__device__ inline void store2<BF16>(void* base, long long offset, float a, float b)
+{
+    const uint32_t lo = __builtin_bit_cast(uint32_t, bf16_round(a)) >> 16;
+    const uint32_t hi = __builtin_bit_cast(uint32_t, bf16_round(b)) & 0xffff0000u;
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(base) + offset) = lo | hi;
+}
+
+// ---------------------------------------------------------------- parameters
+
 struct AttnParams
 {
     PlanArgs plan;
@@ -135,172 +223,160 @@ struct AttnParams
     int heads;
     int dim;              // D = heads * 128
     int text_len;
+    int text_pad;         // text_len rounded up to a multiple of kTextPad
     int npairs;           // windows * heads
     int nqb;              // query blocks per (window, head)
     int qk_norm;
     int rope_mode;
     int rope_npos;
     float eps;
-    float scale;          // 1/sqrt(128) in fp32, as the reference computes it
+    float score_log2;     // (1/sqrt(128)) * log2(e): exp(s*scale - m) = exp2(s*score_log2 - m')
     const float* gq_vid;
     const float* gk_vid;
     const float* gq_txt;
     const float* gk_txt;
     const float2* rope_tab; // [3][npos][24] (cos, sin)
     void* vid_out;
-    uint16_t* partial;      // [nwin][text_len][D] bf16 bits
+    uint16_t* partial;      // [nwin][text_len][D] bf16
     float* dbg_pre;         // optional [sum S][D]
+    uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
+    uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
+    uint16_t* txt_vt;       // [heads][128][text_pad] fp16, prepared and transposed
 };
 
-// Where the window-sequence row j of a window lives and how it is rotated.
-struct RowRef
-{
-    const void* base;  // tensor holding the row
-    long long offset;  // element offset of the row start
-    bool valid;
-    bool text;
-    bool rotate;
-    int pos[3];
-};
+// ---------------------------------------------------------------- lane helpers
 
-__device__ inline RowRef resolve_row(const AttnParams& p, const WindowBox& b, int j)
+// Sum over the 16 lanes of a row group: quad xor 1, quad xor 2, half-row
+// mirror, row mirror (DPP), every lane ends with the full sum.
+__device__ inline float row16_sum(float v)
 {
-    RowRef r;
-    r.valid = j < b.vlen + p.text_len;
-    r.text = false;
-    r.rotate = false;
-    r.pos[0] = r.pos[1] = r.pos[2] = 0;
-    r.base = p.vid_qkv;
-    r.offset = 0;
-    if (!r.valid)
-        return r;
-    if (j < b.vlen)
-    {
-        int lt, ly, lx;
-        const int row = window_video_row(p.plan, b, j, &lt, &ly, &lx);
-        r.offset = static_cast<long long>(row) * p.row_stride;
-        if (p.rope_mode == SV2_ROPE_REFERENCE)
-        {
-            // window-local positions, time offset by the text length (:988, :994)
-            r.rotate = true;
-            r.pos[0] = p.text_len + lt;
-            r.pos[1] = ly;
-            r.pos[2] = lx;
-        }
-        else if (p.rope_mode == SV2_ROPE_ABSOLUTE)
-        {
-            r.rotate = true;
-            r.pos[0] = b.t0 + lt;
-            r.pos[1] = b.h0 + ly;
-            r.pos[2] = b.w0 + lx;
-        }
-    }
-    else
-    {
-        const int l = j - b.vlen;
-        r.base = p.txt_qkv;
-        r.text = true;
-        r.offset = static_cast<long long>(l) * p.row_stride;
-        if (p.rope_mode == SV2_ROPE_REFERENCE)
-        {
-            // text token l rotated at (l, l, l) (:1004-1020)
-            r.rotate = true;
-            r.pos[0] = r.pos[1] = r.pos[2] = l;
-        }
-    }
-    return r;
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
 }
 
-// RoPE axis and pair of an even head dim, or -1 when the dim is not rotated.
-__device__ inline int rope_slot(int mode, int d, int* pair)
+// The value of lane l and of lane l^32 (ds_bpermute).  Both lanes of a pair
+// then reduce the same two operands, so they agree bit for bit.
+__device__ inline void with_partner(float v, float* a, float* b)
 {
-    if (mode == SV2_ROPE_REFERENCE)
-    {
-        if (d >= 126)
-            return -1;
-        const int axis = d / 42;
-        *pair = (d - axis * 42) >> 1;
-        return axis;
-    }
+    const float w = __shfl_xor(v, 32);
+    const bool low = (threadIdx.x & 32) == 0;
+    *a = low ? v : w;
+    *b = low ? w : v;
+}
+
+__device__ inline float partner_max(float v)
+{
+    float a, b;
+    with_partner(v, &a, &b);
+    return fmaxf(a, b);
+}
+
+__device__ inline float partner_sum(float v)
+{
+    float a, b;
+    with_partner(v, &a, &b);
+    return a + b;
+}
+
+// ---------------------------------------------------------------- prologue
+
+// RoPE axis and table slot of an even head dim.  Dims a variant leaves
+// unrotated (126, 127 of the reference layout) read slot 23, which the table
+// fills with (cos, sin) = (1, 0).
+__device__ inline void rope_axis_slot(int mode, int d, int* axis, int* slot)
+{
     if (mode == SV2_ROPE_ABSOLUTE)
     {
         if (d < 32)
         {
-            *pair = d >> 1;
-            return 0;
+            *axis = 0;
+            *slot = d >> 1;
         }
-        if (d < 80)
+        else if (d < 80)
         {
-            *pair = (d - 32) >> 1;
-            return 1;
+            *axis = 1;
+            *slot = (d - 32) >> 1;
         }
-        *pair = (d - 80) >> 1;
-        return 2;
+        else
+        {
+            *axis = 2;
+            *slot = (d - 80) >> 1;
+        }
+        return;
     }
-    return -1;
+    if (d < 126)
+    {
+        const int a = d / 42;
+        *axis = a;
+        *slot = (d - 42 * a) >> 1;
+    }
+    else
+    {
+        *axis = 2;
+        *slot = kRopePairSlots - 1;
+    }
 }
 
-// The q/k prologue for the 8 dims [d0, d0+8) of one row held by one lane;
-// the 16 lanes of a row group hold its 128 dims (lanes 16g .. 16g+15, all
-// active).  Follows normalize_and_rotate (seedvr2_dit_block.cpp:942-974):
-// double sum of squares, inv = 1/sqrtf(float(ss/128) + eps), y = x*inv*gamma,
-// rotation of adjacent pairs with (cos, sin) of float(pos)*freq, bf16 RNE.
-// Multiplies and adds are kept separate (no contraction), as in the reference.
-__device__ inline void qk_prologue8(float x[8], const float* gamma, int d0, const RowRef& row,
-                                    const AttnParams& p)
+__device__ inline float inv_rms(float ss, float eps)
+{
+    return __builtin_amdgcn_rsqf(ss * (1.f / 128.f) + eps);
+}
+
+// y = x * inv * gamma, then the rotation of the 4 adjacent pairs of the 8
+// dims (seedvr2_dit_block.cpp:950-971).  Multiplies and adds stay separate
+// (no contraction), as the reference evaluates them.  cs(q) gives the (cos,
+// sin) of pair q.
+template <typename CosSin>
+__device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, bool rotate, CosSin cs)
 {
 #pragma clang fp contract(off)
-    if (p.qk_norm)
+    if (norm)
     {
-        double ss = 0.0;
 #pragma unroll
         for (int e = 0; e < 8; e++)
-            ss += static_cast<double>(x[e]) * static_cast<double>(x[e]);
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        ss += __shfl_xor(ss, 8);
-        const float inv = 1.f / sqrtf(static_cast<float>(ss / 128.0) + p.eps);
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            x[e] = x[e] * inv * gamma[d0 + e];
+            x[e] = x[e] * inv * gamma8[e];
     }
-    if (row.rotate)
+    if (rotate)
     {
 #pragma unroll
         for (int q = 0; q < 4; q++)
         {
-            int pair = 0;
-            const int axis = rope_slot(p.rope_mode, d0 + 2 * q, &pair);
-            if (axis >= 0)
-            {
-                const float2 cs = p.rope_tab[(axis * p.rope_npos + row.pos[axis]) * kRopePairSlots + pair];
-                const float first = x[2 * q];
-                const float second = x[2 * q + 1];
-                const float a = first * cs.x;
-                const float b = second * cs.y;
-                const float c = second * cs.x;
-                const float d = first * cs.y;
-                x[2 * q] = a - b;
-                x[2 * q + 1] = c + d;
-            }
+            const float2 c = cs(q);
+            const float first = x[2 * q];
+            const float second = x[2 * q + 1];
+            const float a = first * c.x;
+            const float b = second * c.y;
+            const float cc = second * c.x;
+            const float d = first * c.y;
+            x[2 * q] = a - b;
+            x[2 * q + 1] = cc + d;
         }
     }
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        x[e] = bf16_round(x[e]);
 }
 
-// 8 bf16-exact floats -> 8 bf16 bit patterns packed in a uint4.
-__device__ inline uint4 pack_bf16x8(const float x[8])
+// Prologue of 8 dims of a row whose 128 dims are spread over 16 consecutive
+// lanes (all active): per-head RMSNorm (fp32 sum of squares), gamma, RoPE,
+// bf16 rounding.
+template <typename CosSin>
+__device__ inline uint4 prologue16(float x[8], const float* gamma8, bool rotate, CosSin cs, const AttnParams& p)
 {
-    uint4 v;
-    v.x = (__builtin_bit_cast(uint32_t, x[0]) >> 16) | (__builtin_bit_cast(uint32_t, x[1]) & 0xffff0000u);
-    v.y = (__builtin_bit_cast(uint32_t, x[2]) >> 16) | (__builtin_bit_cast(uint32_t, x[3]) & 0xffff0000u);
-    v.z = (__builtin_bit_cast(uint32_t, x[4]) >> 16) | (__builtin_bit_cast(uint32_t, x[5]) & 0xffff0000u);
-    v.w = (__builtin_bit_cast(uint32_t, x[6]) >> 16) | (__builtin_bit_cast(uint32_t, x[7]) & 0xffff0000u);
-    return v;
+    float inv = 1.f;
+    if (p.qk_norm)
+    {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            ss = __builtin_fmaf(x[e], x[e], ss);
+        inv = inv_rms(row16_sum(ss), p.eps);
+    }
+    scale_rotate8(x, gamma8, inv, p.qk_norm != 0, rotate, cs);
+    return to_bf16x8(x);
 }
+
+// ---------------------------------------------------------------- layout helpers
 
 // Row permutation of a 32-key S^T tile: swapping bits 2 and 3 of the row makes
 // each lane's 16 accumulator registers hold keys 8g..8g+7 and 16+8g..16+8g+7
@@ -311,71 +387,522 @@ __device__ inline int key_perm(int i)
     return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
-// Swizzled offset (in halfs) of key group `grp` (8 keys) in row d of the
-// transposed v tile; spreads the 16-byte reads of consecutive rows over banks.
+// Swizzled offset (in halfs) of key group `grp` (8 keys, 0..7) in row d of the
+// transposed value tile; spreads both the 16-byte reads of 8 consecutive rows
+// and the scattered writes of rows 8 apart over the banks.
 __device__ inline int vt_offset(int d, int grp)
 {
     return d * kVtStride + ((grp ^ ((d ^ (d >> 3)) & 7)) << 3);
 }
 
+// Two values rounded to bf16 (the reference's rounding of v) and handed to the
+// fp16 MFMA: the bf16 values are exact in fp16 within its range.
+__device__ inline f16x2 bf16_pair_as_f16(float a, float b)
+{
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    bf16x2 r;
+    r[0] = static_cast<__bf16>(a);
+    r[1] = static_cast<__bf16>(b);
+    const uint32_t u = __builtin_bit_cast(uint32_t, r);
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, u << 16),
+                                                                __builtin_bit_cast(float, u & 0xffff0000u)));
+}
+
+// ---------------------------------------------------------------- per-window staging
+
+struct WindowLds
+{
+    int2 vrows[kMaxVideoRows];                    // global row, local (t | y<<10 | x<<20)
+    float2 rope[kMaxRopeRows * kRopePairSlots];   // rows t..., y..., x... of the window
+    float gamma[2][kHeadDim];                     // q, k gammas of the video branch
+};
+
+// Row of the staged RoPE table where each axis starts.
+struct RopeBase
+{
+    int b[3];
+};
+
+__device__ inline RopeBase rope_base(const WindowBox& box)
+{
+    RopeBase r;
+    r.b[0] = 0;
+    r.b[1] = box.lt;
+    r.b[2] = box.lt + box.lh;
+    return r;
+}
+
+// Fills the gather table, the window's RoPE rows and the gammas (threads
+// stride by nthreads; the caller synchronises).
+__device__ inline void stage_window(const AttnParams& p, const WindowBox& box, WindowLds& s, int tid, int nthreads)
+{
+    for (int j = tid; j < box.vlen; j += nthreads)
+    {
+        int lt, ly, lx;
+        const int row = window_video_row(p.plan, box, j, &lt, &ly, &lx);
+        s.vrows[j] = make_int2(row, static_cast<int>(static_cast<uint32_t>(lt) | (static_cast<uint32_t>(ly) << 10) |
+                                                     (static_cast<uint32_t>(lx) << 20)));
+    }
+    if (p.rope_mode != SV2_ROPE_NONE)
+    {
+        const int rows = box.lt + box.lh + box.lw;
+        const bool ref = p.rope_mode == SV2_ROPE_REFERENCE;
+        for (int i = tid; i < rows * kRopePairSlots; i += nthreads)
+        {
+            const int r = i / kRopePairSlots;
+            const int slot = i - r * kRopePairSlots;
+            int axis, gpos;
+            if (r < box.lt)
+            {
+                axis = 0;
+                gpos = ref ? p.text_len + r : box.t0 + r; // (L_txt + t - t0) or absolute t
+            }
+            else if (r < box.lt + box.lh)
+            {
+                axis = 1;
+                gpos = (r - box.lt) + (ref ? 0 : box.h0);
+            }
+            else
+            {
+                axis = 2;
+                gpos = (r - box.lt - box.lh) + (ref ? 0 : box.w0);
+            }
+            s.rope[i] = p.rope_tab[(axis * p.rope_npos + gpos) * kRopePairSlots + slot];
+        }
+    }
+    for (int i = tid; i < 2 * kHeadDim; i += nthreads)
+    {
+        const float* src = i < kHeadDim ? p.gq_vid : p.gk_vid;
+        s.gamma[i / kHeadDim][i % kHeadDim] = p.qk_norm ? src[i % kHeadDim] : 1.f;
+    }
+}
+
+// Query operand of S^T = K Q^T for window-sequence row qrow (clamped by the
+// caller to a valid row): lane holds dims 16c + 8g .. +7 of the row, the
+// partner lane (lane ^ 32) the other half.  Video rows run the prologue here;
+// text rows read the prepared workspace.
+template <typename TI>
+__device__ inline void query_operand(const AttnParams& p, const WindowBox& box, const WindowLds& s, int head,
+                                     int qrow, int g, bf16x8 qf[8])
+{
+    const bool is_video = qrow < box.vlen;
+    const long long q_col = static_cast<long long>(head) * kHeadDim;
+    if (!is_video)
+    {
+        const uint16_t* src = p.txt_q + (static_cast<long long>(head) * p.text_len + (qrow - box.vlen)) * kHeadDim;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            qf[c] = *reinterpret_cast<const bf16x8*>(src + 16 * c + 8 * g);
+    }
+    // both lanes of a pair take the same branch; the partner exchange below
+    // runs on every lane
+    float x[64];
+    uint32_t packed = 0u;
+    if (is_video)
+    {
+        const int2 vr = s.vrows[qrow];
+        packed = static_cast<uint32_t>(vr.y);
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 16 * c + 8 * g, &x[8 * c]);
+    }
+    else
+    {
+#pragma unroll
+        for (int i = 0; i < 64; i++)
+            x[i] = 0.f;
+    }
+    float inv = 1.f;
+    if (p.qk_norm)
+    {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 64; i++)
+            ss = __builtin_fmaf(x[i], x[i], ss);
+        inv = inv_rms(partner_sum(ss), p.eps);
+    }
+    if (!is_video)
+        return;
+    const RopeBase rb = rope_base(box);
+    const bool rotate = p.rope_mode != SV2_ROPE_NONE;
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+    {
+        const int d0 = 16 * c + 8 * g;
+        scale_rotate8(&x[8 * c], &s.gamma[0][d0], inv, p.qk_norm != 0, rotate, [&](int q) {
+            int axis, slot;
+            rope_axis_slot(p.rope_mode, d0 + 2 * q, &axis, &slot);
+            const int local = static_cast<int>((packed >> (10 * axis)) & 1023u);
+            return s.rope[(rb.b[axis] + local) * kRopePairSlots + slot];
+        });
+        qf[c] = __builtin_bit_cast(bf16x8, to_bf16x8(&x[8 * c]));
+    }
+}
+
+// Per-thread RoPE lookup of a key chunk: the chunk (8 dims) is fixed per
+// thread, so the table offset of each of its 4 pairs is too; only the row's
+// local position varies.
+struct KeyRope
+{
+    int off[4];
+    int shift[4];
+};
+
+__device__ inline KeyRope key_rope(const AttnParams& p, const RopeBase& rb, int d0)
+{
+    KeyRope k;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+    {
+        int axis, slot;
+        rope_axis_slot(p.rope_mode, d0 + 2 * q, &axis, &slot);
+        k.off[q] = rb.b[axis] * kRopePairSlots + slot;
+        k.shift[q] = 10 * axis;
+    }
+    return k;
+}
+
+// Prologue of one key chunk (8 dims of the row with packed local positions).
+__device__ inline uint4 key_chunk(const AttnParams& p, const WindowLds& s, const KeyRope& kr, float x[8], int d0,
+                                  uint32_t packed)
+{
+    return prologue16(x, &s.gamma[1][d0], p.rope_mode != SV2_ROPE_NONE, [&](int q) {
+        const int local = static_cast<int>((packed >> kr.shift[q]) & 1023u);
+        return s.rope[kr.off[q] + local * kRopePairSlots];
+    }, p);
+}
+
+// ---------------------------------------------------------------- text prepare
+
+// Text tokens: q/k prologue with the text branch's gammas and positions
+// (l, l, l) in the reference RoPE mode (text is not rotated in the absolute
+// mode), v rounded to bf16 and stored as fp16, transposed; zero padding up to
+// text_pad so masked keys multiply finite values.
+template <typename TI>
+__global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
+{
+    const int head = blockIdx.y;
+    const int l = blockIdx.x * kPrepRows + (threadIdx.x >> 4);
+    const int chunk = threadIdx.x & 15;
+    const int d0 = chunk * 8;
+    const bool valid = l < p.text_len;
+    const long long row = static_cast<long long>(valid ? l : 0) * p.row_stride + static_cast<long long>(head) * kHeadDim;
+    float q[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float k[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (valid)
+    {
+        load8<TI>(p.txt_qkv, row + d0, q);
+        load8<TI>(p.txt_qkv, row + p.dim + d0, k);
+        load8<TI>(p.txt_qkv, row + 2LL * p.dim + d0, v);
+    }
+    const bool rotate = p.rope_mode == SV2_ROPE_REFERENCE;
+    const int pos = valid ? l : 0;
+    auto cs = [&](int qq) {
+        int axis, slot;
+        rope_axis_slot(p.rope_mode, d0 + 2 * qq, &axis, &slot);
+        return p.rope_tab[(axis * p.rope_npos + pos) * kRopePairSlots + slot];
+    };
+    float gq[8];
+    float gk[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+    {
+        gq[e] = p.qk_norm ? p.gq_txt[d0 + e] : 1.f;
+        gk[e] = p.qk_norm ? p.gk_txt[d0 + e] : 1.f;
+    }
+    const uint4 qb = prologue16(q, gq, rotate, cs, p);
+    const uint4 kb = prologue16(k, gk, rotate, cs, p);
+    if (l >= p.text_pad)
+        return;
+    if (valid)
+    {
+        const long long o = (static_cast<long long>(head) * p.text_len + l) * kHeadDim + d0;
+        *reinterpret_cast<uint4*>(p.txt_q + o) = qb;
+        *reinterpret_cast<uint4*>(p.txt_k + o) = kb;
+    }
+    _Float16* vt = reinterpret_cast<_Float16*>(p.txt_vt);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+    {
+        const f16x2 h = bf16_pair_as_f16(v[e], v[e + 1]);
+        const long long base = (static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l;
+        vt[base] = valid ? h[0] : static_cast<_Float16>(0.f);
+        vt[base + p.text_pad] = valid ? h[1] : static_cast<_Float16>(0.f);
+    }
+}
+
+// ---------------------------------------------------------------- main kernel
+
+// Registers holding one tile between its global loads and its LDS store.
+// Video tiles: every thread holds two key items (rows r and r+32 of the tile,
+// the same 8 dims) in k0/k1 and one value item (keys 2kp and 2kp+1, 8 dims)
+// in v0/v1.  Text tiles (prepared data): k0/k1 hold key rows r and r+32, v0/v1
+// the value items tid and tid+512 (row of V^T, group of 8 keys).
+template <typename TI>
+struct TileRegs
+{
+    uint4 k0[TI::kVec];
+    uint4 k1[TI::kVec];
+    uint4 v0[TI::kVec];
+    uint4 v1[TI::kVec];
+    uint32_t pk0;
+    uint32_t pk1;
+};
+
+struct Geometry
+{
+    int vlen;   // video keys / queries of the window
+    int seq;    // vlen + text_len
+    int ntb;    // text key tiles (processed first)
+    int nkb;    // all key tiles
+};
+
+// Issues the global loads of key tile kb into registers.  Rows past the end
+// of a ragged tile are clamped to the last valid row: their scores are masked
+// and their values multiply p = 0, so any finite data will do.
+template <typename TI>
+__device__ inline void load_tile(const AttnParams& p, const Geometry& gm, const WindowLds& s, int head, int kb,
+                                 int tid, TileRegs<TI>& t)
+{
+    const int r = tid >> 4;
+    const int chunk = tid & 15;
+    if (kb < gm.ntb)
+    {
+        const int base = kb * kBlockN;
+        const long long kbase = static_cast<long long>(head) * p.text_len;
+        const int l0 = min(base + r, p.text_len - 1);
+        const int l1 = min(base + r + 32, p.text_len - 1);
+        t.k0[0] = *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l0) * kHeadDim + chunk * 8);
+        t.k1[0] = *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l1) * kHeadDim + chunk * 8);
+        const long long vbase = static_cast<long long>(head) * kHeadDim;
+        const int i0 = tid;
+        const int i1 = tid + kThreads;
+        t.v0[0] = *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (i0 >> 3)) * p.text_pad + base + (i0 & 7) * 8);
+        t.v1[0] = *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (i1 >> 3)) * p.text_pad + base + (i1 & 7) * 8);
+        return;
+    }
+    const int base = (kb - gm.ntb) * kBlockN;
+    const long long k_col = static_cast<long long>(p.dim) + static_cast<long long>(head) * kHeadDim + chunk * 8;
+    const long long v_col = k_col + p.dim;
+    const int last = gm.vlen - 1;
+    const int2 a = s.vrows[min(base + r, last)];
+    const int2 b = s.vrows[min(base + r + 32, last)];
+    t.pk0 = static_cast<uint32_t>(a.y);
+    t.pk1 = static_cast<uint32_t>(b.y);
+    load_raw8<TI>(p.vid_qkv, static_cast<long long>(a.x) * p.row_stride + k_col, t.k0);
+    load_raw8<TI>(p.vid_qkv, static_cast<long long>(b.x) * p.row_stride + k_col, t.k1);
+    const int j0 = base + 2 * r; // key pair of this thread's value item
+    const int r0 = s.vrows[min(j0, last)].x;
+    const int r1 = s.vrows[min(j0 + 1, last)].x;
+    load_raw8<TI>(p.vid_qkv, static_cast<long long>(r0) * p.row_stride + v_col, t.v0);
+    load_raw8<TI>(p.vid_qkv, static_cast<long long>(r1) * p.row_stride + v_col, t.v1);
+}
+
+// Runs the prologue on the registers of tile kb and writes them to LDS.
+template <typename TI>
+__device__ inline void store_tile(const AttnParams& p, const Geometry& gm, const WindowLds& s, const KeyRope& kr,
+                                  int kb, int tid, const TileRegs<TI>& t, uint16_t* k_tile, uint16_t* vt_tile)
+{
+    const int r = tid >> 4;
+    const int d0 = (tid & 15) * 8;
+    if (kb < gm.ntb)
+    {
+        *reinterpret_cast<uint4*>(&k_tile[r * kKStride + d0]) = t.k0[0];
+        *reinterpret_cast<uint4*>(&k_tile[(r + 32) * kKStride + d0]) = t.k1[0];
+        const int i0 = tid;
+        const int i1 = tid + kThreads;
+        *reinterpret_cast<uint4*>(&vt_tile[vt_offset(i0 >> 3, i0 & 7)]) = t.v0[0];
+        *reinterpret_cast<uint4*>(&vt_tile[vt_offset(i1 >> 3, i1 & 7)]) = t.v1[0];
+        return;
+    }
+    {
+        float x[8];
+        raw8_to_float<TI>(t.k0, x);
+        *reinterpret_cast<uint4*>(&k_tile[r * kKStride + d0]) = key_chunk(p, s, kr, x, d0, t.pk0);
+    }
+    {
+        float x[8];
+        raw8_to_float<TI>(t.k1, x);
+        *reinterpret_cast<uint4*>(&k_tile[(r + 32) * kKStride + d0]) = key_chunk(p, s, kr, x, d0, t.pk1);
+    }
+    {
+        const int key = 2 * r;
+        float v0[8];
+        float v1[8];
+        raw8_to_float<TI>(t.v0, v0);
+        raw8_to_float<TI>(t.v1, v1);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            *reinterpret_cast<f16x2*>(&vt_tile[vt_offset(d0 + e, key >> 3) + (key & 7)]) = bf16_pair_as_f16(v0[e], v1[e]);
+    }
+}
+
+// One 64-key tile of the online softmax for the wave's 32 query rows.
+__device__ inline void attend_tile(const AttnParams& p, const uint16_t* kt_base, const uint16_t* vt_base,
+                                   const bf16x8 qf[8], int nvalid, int lr, int g, f32x16 o[4], float& m_run,
+                                   float& l_run)
+{
+    // ---- S^T for two 32-key subtiles
+    f32x16 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+    {
+        s[kt] = f32x16{};
+        const uint16_t* krow = kt_base + (kt * 32 + key_perm(lr)) * kKStride + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+        {
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + 16 * c);
+            s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
+        }
+    }
+    // ---- mask ragged tiles, online softmax (row = this lane's query)
+    if (nvalid < kBlockN)
+    {
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+            {
+                const int key = kt * 32 + key_perm(8 * (r >> 2) + 4 * g + (r & 3));
+                if (key >= nvalid)
+                    s[kt][r] = -INFINITY;
+            }
+    }
+    float smax = s[0][0];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            smax = fmaxf(smax, s[kt][r]);
+    const float m_new = fmaxf(m_run, partner_max(smax));
+    // lazy rescale: keep the old reference max unless it is exceeded by more
+    // than 2^8 (p stays <= 256, exact in fp16 and fp32); O / l does not depend
+    // on the reference max
+    const bool grow = (m_new - m_run) * p.score_log2 > kRescaleLog2;
+    if (__any(grow))
+    {
+        if (grow)
+        {
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.score_log2);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                o[dt] *= alpha;
+            m_run = m_new;
+        }
+    }
+    const float bias = m_run * p.score_log2;
+    // ---- P (fp16), row sums from the same fp16 values, O^T += V^T P^T
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; c2++)
+        {
+            f16x8 b;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+            {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * c2 + e], p.score_log2, -bias));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * c2 + e + 1], p.score_log2, -bias));
+                f16x2 h;
+                h[0] = static_cast<_Float16>(p0); // round to nearest even (v_cvt_pk_f16_f32)
+                h[1] = static_cast<_Float16>(p1);
+                b[e] = h[0];
+                b[e + 1] = h[1];
+                l_run = __builtin_amdgcn_fdot2(h, f16x2{static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)}, l_run,
+                                               false);
+            }
+            const int kgrp = kt * 4 + c2 * 2 + g;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+            {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(vt_base + vt_offset(dt * 32 + lr, kgrp));
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[dt], 0, 0, 0);
+            }
+        }
+}
+
+// Query rows of one workgroup: a window of S rows is split into
+// ceil(S / 256) blocks of equal size (rounded up to 32 rows), so a large
+// window keeps all its query waves busy.
+struct QueryBlock
+{
+    int q0;
+    int q1;
+};
+
+__device__ inline QueryBlock query_block(int seq, int qb)
+{
+    const int nqb = (seq + kRowsPerGroup - 1) / kRowsPerGroup;
+    const int per = ((seq + nqb - 1) / nqb + 31) / 32 * 32;
+    QueryBlock b;
+    b.q0 = qb * per;
+    b.q1 = min(b.q0 + per, seq);
+    return b;
+}
+
 template <typename TI, typename TO>
 __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t q_tile[kBlockM * kQkStride];
-    __shared__ __attribute__((aligned(16))) uint16_t k_tile[kBlockN * kQkStride];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_tile[kHeadDim * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t k_tiles[2][kBlockN * kKStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_tiles[2][kHeadDim * kVtStride];
+    __shared__ WindowLds lds;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // XCD-aware decode: workgroup ids go round-robin over the 8 XCDs, so
-    // ids x, x+8, x+16 ... share an XCD (and its L2).  The query blocks of one
-    // (window, head) pair are consecutive on one XCD, so the K/V rows they all
-    // read come from that XCD's L2 after the first read from HBM.
+    // XCD-aware decode: workgroup ids go round-robin over the 8 XCDs; the query
+    // blocks of one (window, head) pair are consecutive ids of one XCD, run
+    // side by side and share its L2 for the key/value rows they both read.
     const int id = blockIdx.x;
     const int xcd = id & 7;
     const int slot = id >> 3;
-    const int pair = (slot / p.nqb) * 8 + xcd;
-    const int qb = slot - (slot / p.nqb) * p.nqb;
+    const int grp = slot / p.nqb;
+    const int pair = grp * 8 + xcd;
+    const int qb = slot - grp * p.nqb;
     if (pair >= p.npairs)
         return;
     const int wi = pair / p.heads;
     const int head = pair - wi * p.heads;
     const WindowBox box = window_box(p.plan, wi);
-    const int seq = box.vlen + p.text_len;
-    const int q0 = qb * kBlockM;
-    if (q0 >= seq)
+    Geometry gm;
+    gm.vlen = box.vlen;
+    gm.seq = box.vlen + p.text_len;
+    gm.ntb = (p.text_len + kBlockN - 1) / kBlockN;
+    gm.nkb = gm.ntb + (box.vlen + kBlockN - 1) / kBlockN;
+    const QueryBlock qbk = query_block(gm.seq, qb);
+    if (qbk.q0 >= gm.seq)
         return;
 
-    const int rsub = tid >> 4;  // row within a 16-row pass
-    const int chunk = tid & 15; // 8-dim slice of the row
-    const int d0 = chunk * 8;
-    const long long q_col = static_cast<long long>(head) * kHeadDim;
-    const long long k_col = q_col + p.dim;
-    const long long v_col = q_col + 2LL * p.dim;
-
-    // ---- query tile: prologue in registers, bf16 into LDS
-    for (int pass = 0; pass < kBlockM / 16; pass++)
-    {
-        const int r = pass * 16 + rsub;
-        const RowRef row = resolve_row(p, box, q0 + r);
-        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (row.valid)
-            load8<TI>(row.base, row.offset + q_col + d0, x);
-        qk_prologue8(x, row.text ? p.gq_txt : p.gq_vid, d0, row, p);
-        *reinterpret_cast<uint4*>(&q_tile[r * kQkStride + d0]) = pack_bf16x8(x);
-    }
+    stage_window(p, box, lds, tid, kThreads);
     __syncthreads();
 
-    const int g = lane >> 5;
     const int lr = lane & 31;
-    // B operand of S^T = K Q^T: lane holds query lr, dims 16c + 8g .. +7
+    const int g = lane >> 5;
+    const bool wave_active = qbk.q0 + wave * 32 < qbk.q1;
+    const int qrow = qbk.q0 + wave * 32 + lr;
+    const KeyRope kr = key_rope(p, rope_base(box), (tid & 15) * 8);
+
     bf16x8 qf[8];
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-        qf[c] = *reinterpret_cast<const bf16x8*>(&q_tile[(wave * 32 + lr) * kQkStride + 16 * c + 8 * g]);
-    const bool wave_active = q0 + wave * 32 < seq;
+    query_operand<TI>(p, box, lds, head, min(qrow, gm.seq - 1), g, qf);
+    // every query load completes here, before any tile load is issued: with
+    // nothing older pending, the waits the compiler places in front of the
+    // MFMAs that read qf do not drain the tile prefetches below
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
+    // three tiles in flight: loads of tile kb+3 are issued while tile kb is
+    // consumed, into the registers tile kb occupied (stored two steps before).
+    // Every step issues its loads (past the last tile they repeat the last
+    // one, an L2 hit), so the number of loads in flight is the same on every
+    // path and each store waits only for the tile it stores.
+    const int last_tile = gm.nkb - 1;
+    TileRegs<TI> ra, rb, rc;
+    load_tile<TI>(p, gm, lds, head, 0, tid, ra);
+    load_tile<TI>(p, gm, lds, head, min(1, last_tile), tid, rb);
+    load_tile<TI>(p, gm, lds, head, min(2, last_tile), tid, rc);
 
     f32x16 o[4];
 #pragma unroll
@@ -384,141 +911,45 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    const int nkb = (seq + kBlockN - 1) / kBlockN;
-    for (int kb = 0; kb < nkb; kb++)
-    {
-        __syncthreads(); // previous tile fully consumed
+    store_tile<TI>(p, gm, lds, kr, 0, tid, ra, k_tiles[0], vt_tiles[0]);
+    __syncthreads();
 
-        // ---- key tile: prologue in registers, bf16 into LDS
-#pragma unroll
-        for (int pass = 0; pass < kBlockN / 16; pass++)
-        {
-            const int r = pass * 16 + rsub;
-            const RowRef row = resolve_row(p, box, kb * kBlockN + r);
-            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (row.valid)
-                load8<TI>(row.base, row.offset + k_col + d0, x);
-            qk_prologue8(x, row.text ? p.gk_txt : p.gk_vid, d0, row, p);
-            *reinterpret_cast<uint4*>(&k_tile[r * kQkStride + d0]) = pack_bf16x8(x);
-        }
-        // ---- value tile: bf16 rounding, fp16 operands, transposed into LDS;
-        // thread = 4 consecutive keys x one 8-dim slice
-        {
-            const int kg = tid >> 4;
-            float v[4][8];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-            {
-                const RowRef row = resolve_row(p, box, kb * kBlockN + 4 * kg + i);
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    v[i][e] = 0.f;
-                if (row.valid)
-                    load8<TI>(row.base, row.offset + v_col + d0, v[i]);
-            }
-            typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-            {
-                f16x4 h;
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    h[i] = static_cast<_Float16>(bf16_round(v[i][e]));
-                const int d = d0 + e;
-                *reinterpret_cast<f16x4*>(&vt_tile[vt_offset(d, kg >> 1) + (kg & 1) * 4]) = h;
-            }
-        }
+    auto valid_keys = [&](int kb) {
+        return kb < gm.ntb ? p.text_len - kb * kBlockN : gm.vlen - (kb - gm.ntb) * kBlockN;
+    };
+    // step kb: attend tile kb, store tile kb+1 from `next`, reload `cur`
+    // (which held tile kb) with tile kb+3
+    auto step = [&](int kb, TileRegs<TI>& cur, TileRegs<TI>& next) {
+        const int buf = kb & 1;
+        if (kb < gm.nkb && wave_active)
+            attend_tile(p, k_tiles[buf], vt_tiles[buf], qf, valid_keys(kb), lr, g, o, m_run, l_run);
+        if (kb + 1 < gm.nkb)
+            store_tile<TI>(p, gm, lds, kr, kb + 1, tid, next, k_tiles[buf ^ 1], vt_tiles[buf ^ 1]);
+        load_tile<TI>(p, gm, lds, head, min(kb + 3, last_tile), tid, cur);
         __syncthreads();
-
-        if (wave_active)
-        {
-            // ---- S^T for two 32-key subtiles
-            f32x16 s[2];
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-            {
-                s[kt] = f32x16{};
-                const uint16_t* krow = &k_tile[(kt * 32 + key_perm(lr)) * kQkStride + 8 * g];
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-                {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + 16 * c);
-                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
-                }
-            }
-            // ---- scale, mask, online softmax (row = this lane's query)
-            float smax = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                {
-                    const int i = 8 * (r >> 2) + 4 * g + (r & 3);
-                    const int key = kb * kBlockN + kt * 32 + key_perm(i);
-                    const float val = key < seq ? s[kt][r] * p.scale : -INFINITY;
-                    s[kt][r] = val;
-                    smax = fmaxf(smax, val);
-                }
-            smax = fmaxf(smax, __shfl_xor(smax, 32));
-            const float m_new = fmaxf(m_run, smax);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
-            const float bias = m_new * kLog2e;
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-                o[dt] *= alpha;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                {
-                    const float e = __builtin_amdgcn_exp2f(s[kt][r] * kLog2e - bias);
-                    s[kt][r] = e;
-                    l_run += e;
-                }
-            // ---- O^T += V^T P^T
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int c2 = 0; c2 < 2; c2++)
-                {
-                    f16x8 b;
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        b[e] = static_cast<_Float16>(s[kt][8 * c2 + e]);
-                    const int grp = kt * 4 + c2 * 2 + g;
-#pragma unroll
-                    for (int dt = 0; dt < 4; dt++)
-                    {
-                        const f16x8 a = *reinterpret_cast<const f16x8*>(&vt_tile[vt_offset(dt * 32 + lr, grp)]);
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[dt], 0, 0, 0);
-                    }
-                }
-        }
+    };
+    for (int kb = 0; kb < gm.nkb; kb += 3)
+    {
+        step(kb, ra, rb);
+        step(kb + 1, rb, rc);
+        step(kb + 2, rc, ra);
     }
 
     if (!wave_active)
         return;
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const int j = q0 + wave * 32 + lr;
-    if (j >= seq)
+    const float l_tot = partner_sum(l_run);
+    if (qrow >= qbk.q1)
         return;
     const float inv_l = 1.f / l_tot;
-    const long long pre_row = p.dbg_pre
-                                  ? (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + j) * p.dim
-                                  : 0;
+    const long long q_col = static_cast<long long>(head) * kHeadDim;
+    const bool text = qrow >= gm.vlen;
     long long out_off;
-    bool text = j >= box.vlen;
     if (!text)
-    {
-        int lt, ly, lx;
-        out_off = static_cast<long long>(window_video_row(p.plan, box, j, &lt, &ly, &lx)) * p.dim + q_col;
-    }
+        out_off = static_cast<long long>(lds.vrows[qrow].x) * p.dim + q_col;
     else
-    {
-        out_off = (static_cast<long long>(wi) * p.text_len + (j - box.vlen)) * p.dim + q_col;
-    }
+        out_off = (static_cast<long long>(wi) * p.text_len + (qrow - gm.vlen)) * p.dim + q_col;
+    const long long pre_row =
+        (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + qrow) * p.dim + q_col;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -534,7 +965,7 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
                 rounded[e] = bf16_round(pre[e]);
             }
             if (p.dbg_pre)
-                store4<F32>(p.dbg_pre, pre_row + q_col + d, pre);
+                store4<F32>(p.dbg_pre, pre_row + d, pre);
             if (!text)
                 store4<TO>(p.vid_out, out_off + d, rounded);
             else
@@ -543,36 +974,51 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
 }
 
 // Text outputs: sum of the per-window bf16 partials in window order, then a
-// multiply by 1/nW (seedvr2_dit_block.cpp:1074-1075, :1081-1088).
+// multiply by 1/nW (seedvr2_dit_block.cpp:1074-1075, :1081-1088).  Each thread
+// owns two elements; the loads of 16 windows are issued before their adds so
+// the sequential sum does not serialise on memory latency.
 template <typename TO>
-__global__ __launch_bounds__(256) void text_window_reduce_kernel(const uint16_t* partial, void* out, int nwin,
-                                                                 long long count, float inv_nw)
+__global__ __launch_bounds__(256) void text_window_reduce_kernel(const uint32_t* partial, void* out, int nwin,
+                                                                 long long pairs, float inv_nw)
 {
-    const long long i = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 4;
-    if (i >= count)
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= pairs)
         return;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < nwin; w++)
+    float a0 = 0.f;
+    float a1 = 0.f;
+    int w = 0;
+    for (; w + 16 <= nwin; w += 16)
     {
-        const uint2 v = *reinterpret_cast<const uint2*>(partial + static_cast<long long>(w) * count + i);
-        acc[0] += __builtin_bit_cast(float, v.x << 16);
-        acc[1] += __builtin_bit_cast(float, v.x & 0xffff0000u);
-        acc[2] += __builtin_bit_cast(float, v.y << 16);
-        acc[3] += __builtin_bit_cast(float, v.y & 0xffff0000u);
-    }
-    float r[4];
+        uint32_t v[16];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-        r[e] = acc[e] * inv_nw;
-    store4<TO>(out, i, r);
+        for (int u = 0; u < 16; u++)
+            v[u] = partial[static_cast<long long>(w + u) * pairs + i];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+        {
+            a0 += __builtin_bit_cast(float, v[u] << 16);
+            a1 += __builtin_bit_cast(float, v[u] & 0xffff0000u);
+        }
+    }
+    for (; w < nwin; w++)
+    {
+        const uint32_t v = partial[static_cast<long long>(w) * pairs + i];
+        a0 += __builtin_bit_cast(float, v << 16);
+        a1 += __builtin_bit_cast(float, v & 0xffff0000u);
+    }
+    store2<TO>(out, 2 * i, a0 * inv_nw, a1 * inv_nw);
 }
 
-// Debug / test: the prologue alone, 16 rows per workgroup, fp32 outputs in
-// window-sequence order.  Same row resolution and prologue code as above.
+// Debug / test: q, k, v after the prologue, fp32, window-sequence order, from
+// the device functions the attention kernel runs: queries through the MFMA
+// operand-layout path, keys 16 lanes per row, values as the fp16 operands;
+// text rows from the prepared workspace.  One workgroup (4 waves) per
+// (window, head, 32 rows).
 template <typename TI>
 __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb, float* q_out, float* k_out,
                                                           float* v_out)
 {
+    __shared__ WindowLds lds;
     const int blk = blockIdx.x;
     const int rb = blk % nrb;
     const int rest = blk / nrb;
@@ -580,33 +1026,71 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
     const int wi = rest / p.heads;
     const WindowBox box = window_box(p.plan, wi);
     const int seq = box.vlen + p.text_len;
-    if (rb * 16 >= seq)
+    if (rb * 32 >= seq)
         return;
     const int tid = threadIdx.x;
-    const int j = rb * 16 + (tid >> 4);
-    const int d0 = (tid & 15) * 8;
-    const RowRef row = resolve_row(p, box, j);
+    stage_window(p, box, lds, tid, 256);
+    __syncthreads();
     const long long q_col = static_cast<long long>(head) * kHeadDim;
-    float q[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float k[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (row.valid)
+    const long long seq_base = static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len;
+
+    if (tid < 64)
     {
-        load8<TI>(row.base, row.offset + q_col + d0, q);
-        load8<TI>(row.base, row.offset + q_col + p.dim + d0, k);
-        load8<TI>(row.base, row.offset + q_col + 2LL * p.dim + d0, v);
-    }
-    qk_prologue8(q, row.text ? p.gq_txt : p.gq_vid, d0, row, p);
-    qk_prologue8(k, row.text ? p.gk_txt : p.gk_vid, d0, row, p);
-    if (!row.valid)
-        return;
-    const long long base = (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + j) * p.dim + q_col + d0;
+        const int lr = tid & 31;
+        const int g = tid >> 5;
+        const int j = rb * 32 + lr;
+        bf16x8 qf[8];
+        query_operand<TI>(p, box, lds, head, min(j, seq - 1), g, qf);
+        if (j < seq)
+        {
 #pragma unroll
-    for (int e = 0; e < 8; e++)
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    q_out[(seq_base + j) * p.dim + q_col + 16 * c + 8 * g + e] = static_cast<float>(qf[c][e]);
+        }
+    }
+    const int d0 = (tid & 15) * 8;
+    const KeyRope kr = key_rope(p, rope_base(box), d0);
+    for (int pass = 0; pass < 2; pass++)
     {
-        q_out[base + e] = q[e];
-        k_out[base + e] = k[e];
-        v_out[base + e] = bf16_round(v[e]);
+        const int j = rb * 32 + pass * 16 + (tid >> 4);
+        const bool valid = j < seq;
+        const int jc = min(j, seq - 1);
+        const long long o = (seq_base + j) * p.dim + q_col + d0;
+        if (jc < box.vlen)
+        {
+            const int2 vr = lds.vrows[jc];
+            float k[8];
+            float v[8];
+            load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + p.dim + d0, k);
+            load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 2LL * p.dim + d0, v);
+            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk(p, lds, kr, k, d0, static_cast<uint32_t>(vr.y)));
+            if (valid)
+            {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                {
+                    const f16x2 h = bf16_pair_as_f16(v[e], v[e + 1]);
+                    k_out[o + e] = static_cast<float>(kb[e]);
+                    k_out[o + e + 1] = static_cast<float>(kb[e + 1]);
+                    v_out[o + e] = static_cast<float>(h[0]);
+                    v_out[o + e + 1] = static_cast<float>(h[1]);
+                }
+            }
+        }
+        else if (valid)
+        {
+            const int l = jc - box.vlen;
+            const uint16_t* ks = p.txt_k + (static_cast<long long>(head) * p.text_len + l) * kHeadDim + d0;
+            const _Float16* vs = reinterpret_cast<const _Float16*>(p.txt_vt);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+            {
+                k_out[o + e] = __builtin_bit_cast(float, static_cast<uint32_t>(ks[e]) << 16);
+                v_out[o + e] = static_cast<float>(vs[(static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l]);
+            }
+        }
     }
 }
 
@@ -620,9 +1104,41 @@ __global__ __launch_bounds__(256) void window_index_map_kernel(PlanArgs plan, in
     }
 }
 
+// ---------------------------------------------------------------- host side
+
 int dtype_ok(int t)
 {
     return t == SV2_F32 || t == SV2_F16 || t == SV2_BF16;
+}
+
+struct Workspace
+{
+    int64_t partial;
+    int64_t txt_q;
+    int64_t txt_k;
+    int64_t txt_vt;
+    int64_t total;
+};
+
+int64_t align256(int64_t v)
+{
+    return (v + 255) & ~int64_t(255);
+}
+
+Workspace workspace_layout(const AttnParams& p)
+{
+    Workspace w;
+    int64_t off = 0;
+    w.partial = off;
+    off = align256(off + static_cast<int64_t>(p.plan.nwin) * p.text_len * p.dim * 2);
+    w.txt_q = off;
+    off = align256(off + static_cast<int64_t>(p.heads) * p.text_len * kHeadDim * 2);
+    w.txt_k = off;
+    off = align256(off + static_cast<int64_t>(p.heads) * p.text_len * kHeadDim * 2);
+    w.txt_vt = off;
+    off = align256(off + static_cast<int64_t>(p.heads) * kHeadDim * p.text_pad * 2);
+    w.total = p.text_len > 0 ? off : 0;
+    return w;
 }
 
 // Validates the attention arguments and fills the kernel parameters.
@@ -640,8 +1156,8 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
         return set_error(SV2_EINVAL, "attention: unknown rope mode");
     if (!a->vid_qkv || (a->text_len > 0 && !a->txt_qkv))
         return set_error(SV2_EINVAL, "attention: null qkv pointer");
-    if (a->qk_norm && (!a->gamma_q_vid || !a->gamma_k_vid || (a->text_len > 0 && (!a->gamma_q_txt || !a->gamma_k_txt))))
-        return set_error(SV2_EINVAL, "attention: qk_norm needs all four gamma vectors");
+    if (a->qk_norm && (!a->gamma_q_vid || !a->gamma_k_vid))
+        return set_error(SV2_EINVAL, "attention: qk_norm needs the video gamma vectors");
     std::memset(p, 0, sizeof(*p));
     int rc = build_plan(a->rule, &p->plan);
     if (rc != SV2_OK)
@@ -656,20 +1172,31 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
     }
     int smax = 0;
     for (int wi = 0; wi < p->plan.nwin; wi++)
-        smax = std::max(smax, window_box(p->plan, wi).vlen + a->text_len);
+    {
+        const WindowBox b = window_box(p->plan, wi);
+        if (b.vlen > kMaxVideoRows)
+            return set_error(SV2_EUNSUPPORTED, "attention: a window holds more than 4096 video tokens");
+        if (b.lt + b.lh + b.lw > kMaxRopeRows || b.lt > 1023 || b.lh > 1023 || b.lw > 1023)
+            return set_error(SV2_EUNSUPPORTED, "attention: window extents beyond the staged RoPE rows (t+h+w <= 160)");
+        smax = std::max(smax, b.vlen + a->text_len);
+    }
+    const int64_t qkv_elems = static_cast<int64_t>(a->rule.frames) * a->rule.height * a->rule.width * 3 * a->heads * kHeadDim;
+    if (qkv_elems >= (int64_t(1) << 40))
+        return set_error(SV2_EUNSUPPORTED, "attention: qkv tensor too large");
     p->vid_qkv = a->vid_qkv;
     p->txt_qkv = a->txt_qkv;
     p->dim = a->heads * kHeadDim;
     p->row_stride = 3LL * p->dim;
     p->heads = a->heads;
     p->text_len = a->text_len;
+    p->text_pad = (a->text_len + kTextPad - 1) / kTextPad * kTextPad;
     p->npairs = p->plan.nwin * a->heads;
-    p->nqb = (smax + kBlockM - 1) / kBlockM;
+    p->nqb = (smax + kRowsPerGroup - 1) / kRowsPerGroup;
     p->qk_norm = a->qk_norm ? 1 : 0;
     p->rope_mode = a->rope_mode;
     p->rope_npos = a->rope_npos;
     p->eps = a->eps;
-    p->scale = 1.f / std::sqrt(static_cast<float>(kHeadDim));
+    p->score_log2 = (1.f / std::sqrt(static_cast<float>(kHeadDim))) * kLog2e;
     p->gq_vid = a->gamma_q_vid;
     p->gk_vid = a->gamma_k_vid;
     p->gq_txt = a->gamma_q_txt ? a->gamma_q_txt : a->gamma_q_vid;
@@ -681,10 +1208,24 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
     return SV2_OK;
 }
 
-int64_t workspace_bytes(const AttnParams& p)
+int bind_workspace(const sv2_attn_args* a, AttnParams* p)
 {
-    const int64_t bytes = static_cast<int64_t>(p.plan.nwin) * p.text_len * p.dim * 2;
-    return (bytes + 255) & ~int64_t(255);
+    const Workspace w = workspace_layout(*p);
+    if (w.total > 0 && (!a->workspace || static_cast<int64_t>(a->workspace_bytes) < w.total))
+        return set_error(SV2_EINVAL, "attention: workspace missing or too small");
+    char* base = static_cast<char*>(a->workspace);
+    p->partial = reinterpret_cast<uint16_t*>(base + w.partial);
+    p->txt_q = reinterpret_cast<uint16_t*>(base + w.txt_q);
+    p->txt_k = reinterpret_cast<uint16_t*>(base + w.txt_k);
+    p->txt_vt = reinterpret_cast<uint16_t*>(base + w.txt_vt);
+    return SV2_OK;
+}
+
+template <typename TI>
+void launch_text_prepare(const AttnParams& p, hipStream_t stream)
+{
+    const dim3 grid((p.text_pad + kPrepRows - 1) / kPrepRows, p.heads);
+    hipLaunchKernelGGL(text_prepare_kernel<TI>, grid, dim3(256), 0, stream, p);
 }
 
 template <typename TI, typename TO>
@@ -696,14 +1237,26 @@ void launch_attention(const AttnParams& p, hipStream_t stream)
 }
 
 template <typename TI>
-void launch_attention_in(const AttnParams& p, int out_dtype, hipStream_t stream)
+void launch_all(const AttnParams& p, int out_dtype, hipStream_t stream)
 {
+    if (p.text_len > 0)
+        launch_text_prepare<TI>(p, stream);
     if (out_dtype == SV2_F32)
         launch_attention<TI, F32>(p, stream);
     else if (out_dtype == SV2_F16)
         launch_attention<TI, F16>(p, stream);
     else
         launch_attention<TI, BF16>(p, stream);
+}
+
+template <typename TO>
+void launch_reduce(const AttnParams& p, void* out, hipStream_t stream)
+{
+    const long long pairs = static_cast<long long>(p.text_len) * p.dim / 2;
+    const unsigned grid = static_cast<unsigned>((pairs + 255) / 256);
+    const float inv_nw = 1.f / static_cast<float>(p.plan.nwin);
+    hipLaunchKernelGGL(text_window_reduce_kernel<TO>, dim3(grid), dim3(256), 0, stream,
+                       reinterpret_cast<const uint32_t*>(p.partial), out, p.plan.nwin, pairs, inv_nw);
 }
 
 } // namespace
@@ -719,7 +1272,7 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args)
     const int rc = prepare(args, &p, &smax);
     if (rc != SV2_OK)
         return rc;
-    return workspace_bytes(p);
+    return workspace_layout(p).total;
 }
 
 int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
@@ -732,36 +1285,28 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
         return rc;
     if (!args->vid_out || (args->text_len > 0 && !args->txt_out))
         return set_error(SV2_EINVAL, "attention: null output pointer");
-    const int64_t need = workspace_bytes(p);
-    if (need > 0 && (!args->workspace || static_cast<int64_t>(args->workspace_bytes) < need))
-        return set_error(SV2_EINVAL, "attention: workspace missing or too small");
-    p.partial = static_cast<uint16_t*>(args->workspace);
+    if ((rc = bind_workspace(args, &p)) != SV2_OK)
+        return rc;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
 
     if (args->qkv_dtype == SV2_F32)
-        launch_attention_in<F32>(p, args->out_dtype, stream);
+        launch_all<F32>(p, args->out_dtype, stream);
     else if (args->qkv_dtype == SV2_F16)
-        launch_attention_in<F16>(p, args->out_dtype, stream);
+        launch_all<F16>(p, args->out_dtype, stream);
     else
-        launch_attention_in<BF16>(p, args->out_dtype, stream);
+        launch_all<BF16>(p, args->out_dtype, stream);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
-        return hip_error(err, "window_attention_kernel launch");
+        return hip_error(err, "window attention launch");
 
     if (p.text_len > 0)
     {
-        const long long count = static_cast<long long>(p.text_len) * p.dim;
-        const unsigned grid = static_cast<unsigned>((count / 4 + 255) / 256);
-        const float inv_nw = 1.f / static_cast<float>(p.plan.nwin);
         if (args->out_dtype == SV2_F32)
-            hipLaunchKernelGGL(text_window_reduce_kernel<F32>, dim3(grid), dim3(256), 0, stream, p.partial,
-                               args->txt_out, p.plan.nwin, count, inv_nw);
+            launch_reduce<F32>(p, args->txt_out, stream);
         else if (args->out_dtype == SV2_F16)
-            hipLaunchKernelGGL(text_window_reduce_kernel<F16>, dim3(grid), dim3(256), 0, stream, p.partial,
-                               args->txt_out, p.plan.nwin, count, inv_nw);
+            launch_reduce<F16>(p, args->txt_out, stream);
         else
-            hipLaunchKernelGGL(text_window_reduce_kernel<BF16>, dim3(grid), dim3(256), 0, stream, p.partial,
-                               args->txt_out, p.plan.nwin, count, inv_nw);
+            launch_reduce<BF16>(p, args->txt_out, stream);
         err = hipGetLastError();
         if (err != hipSuccess)
             return hip_error(err, "text_window_reduce_kernel launch");
@@ -774,23 +1319,37 @@ int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float
     using namespace sv2;
     AttnParams p;
     int smax = 0;
-    const int rc = prepare(args, &p, &smax);
+    int rc = prepare(args, &p, &smax);
     if (rc != SV2_OK)
         return rc;
     if (!q_out || !k_out || !v_out)
         return set_error(SV2_EINVAL, "qk_prologue: null output pointer");
-    const int nrb = (smax + 15) / 16;
+    if ((rc = bind_workspace(args, &p)) != SV2_OK)
+        return rc;
+    const int nrb = (smax + 31) / 32;
     const unsigned grid = static_cast<unsigned>(p.plan.nwin) * p.heads * nrb;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (args->qkv_dtype == SV2_F32)
+    {
+        if (p.text_len > 0)
+            launch_text_prepare<F32>(p, stream);
         hipLaunchKernelGGL(qk_prologue_kernel<F32>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
+    }
     else if (args->qkv_dtype == SV2_F16)
+    {
+        if (p.text_len > 0)
+            launch_text_prepare<F16>(p, stream);
         hipLaunchKernelGGL(qk_prologue_kernel<F16>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
+    }
     else
+    {
+        if (p.text_len > 0)
+            launch_text_prepare<BF16>(p, stream);
         hipLaunchKernelGGL(qk_prologue_kernel<BF16>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
+    }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
-        return hip_error(err, "qk_prologue_kernel launch");
+        return hip_error(err, "qk_prologue launch");
     return SV2_OK;
 }
 

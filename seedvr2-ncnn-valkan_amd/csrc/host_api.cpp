@@ -200,15 +200,22 @@ int sv2_rope_table_build(int rope_mode, const float* freqs, float theta, int npo
     {
         return set_error(SV2_EINVAL, "sv2_rope_table_build: unknown rope mode");
     }
-    std::memset(host_table, 0, sizeof(float) * sv2_rope_table_floats(npos));
     for (int a = 0; a < 3; a++)
         for (int pos = 0; pos < npos; pos++)
-            for (int p = 0; p < pairs[a]; p++)
+            for (int p = 0; p < kRopePairSlots; p++)
             {
+                float* slot = host_table + ((static_cast<size_t>(a) * npos + pos) * kRopePairSlots + p) * 2;
+                if (p >= pairs[a])
+                {
+                    // unused slots rotate by zero: dims the variant leaves
+                    // unrotated (126, 127 of the reference layout) read one
+                    slot[0] = 1.f;
+                    slot[1] = 0.f;
+                    continue;
+                }
                 // float(pos) * freq in fp32, then the C library's cosf / sinf:
                 // the reference evaluates std::cos / std::sin of that float
                 const float angle = static_cast<float>(pos) * freq[a][p];
-                float* slot = host_table + ((static_cast<size_t>(a) * npos + pos) * kRopePairSlots + p) * 2;
                 slot[0] = std::cos(angle);
                 slot[1] = std::sin(angle);
             }

@@ -238,18 +238,22 @@ class WindowAttention:
         return check(load().sv2_window_attention_workspace(ctypes.byref(a)),
                      "sv2_window_attention_workspace")
 
-    def __call__(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
+    def _bind_workspace(self, a: AttnArgs, device) -> None:
         import torch
-        a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
         need = self.workspace_bytes(a)
         if need > 0 and (self.workspace is None or self.workspace.numel() < need):
-            self.workspace = torch.empty(need, dtype=torch.uint8, device=vid_qkv.device)
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=device)
         a.workspace = None if need == 0 else self.workspace.data_ptr()
         a.workspace_bytes = need
+
+    def __call__(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
+        a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
+        self._bind_workspace(a, vid_qkv.device)
         check(load().sv2_window_attention(ctypes.byref(a), _stream(stream)), "sv2_window_attention")
 
     def prologue(self, vid_qkv, txt_qkv, gammas, q_out, k_out, v_out, stream=None):
         a = self.args(vid_qkv, txt_qkv, gammas, q_out, None)
+        self._bind_workspace(a, vid_qkv.device)
         check(load().sv2_qk_prologue(ctypes.byref(a), _ptr(q_out), _ptr(k_out), _ptr(v_out),
                                      _stream(stream)), "sv2_qk_prologue")
 
