@@ -76,6 +76,7 @@ def load() -> ctypes.CDLL:
     vp, i = ctypes.c_void_p, ctypes.c_int
     lib.orc_bf16.argtypes = [ctypes.c_float]
     lib.orc_bf16.restype = ctypes.c_float
+    lib.orc_bf16_array.argtypes = [vp, vp, ctypes.c_int64]
     lib.orc_adaptive_window.argtypes = [i, i, i, vp, vp, vp]
     lib.orc_make_windows.argtypes = [i, i, i, i, i, i, i, vp, i]
     lib.orc_make_windows.restype = i
@@ -103,6 +104,13 @@ def _p(a):
 
 def bf16(x: float) -> float:
     return load().orc_bf16(ctypes.c_float(x))
+
+
+def bf16_array(x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    load().orc_bf16_array(_p(x), _p(out), x.size)
+    return out
 
 
 def adaptive_window(T, H, W):

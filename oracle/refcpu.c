@@ -27,6 +27,12 @@ float orc_bf16(float value)
     return value;
 }
 
+void orc_bf16_array(const float* in, float* out, int64_t count)
+{
+    for (int64_t i = 0; i < count; i++)
+        out[i] = orc_bf16(in[i]);
+}
+
 static int ceil_div_i(int value, int divisor) { return (value + divisor - 1) / divisor; }
 static int min_i(int a, int b) { return a < b ? a : b; }
 static int max_i(int a, int b) { return a > b ? a : b; }

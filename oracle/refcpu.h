@@ -54,6 +54,9 @@ enum {
 /* bf16 round-to-nearest-even kept in an fp32 container (seedvr2_dit_block.cpp:68-79). */
 float orc_bf16(float value);
 
+/* orc_bf16 over an array (for exhaustive tests of the rounding rule). */
+void orc_bf16_array(const float* in, float* out, int64_t count);
+
 /* Adaptive window size rule (seedvr2_dit_block.cpp:832-838). */
 void orc_adaptive_window(int T, int H, int W, int* wt, int* wh, int* ww);
 
