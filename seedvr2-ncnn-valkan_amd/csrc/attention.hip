@@ -6,25 +6,29 @@
 //
 //   text_prepare_kernel   the q/k prologue of the L_txt text tokens, once per
 //                         layer (their RoPE positions (l, l, l) do not depend
-//                         on the window), bf16 q/k and transposed fp16 v into
+//                         on the window): bf16 q/k and transposed fp16 v into
 //                         the workspace;
 //   window_attention_kernel
-//                         one 8-wave workgroup per (window, head) and up to
-//                         256 query rows (larger windows split evenly): every video row of the window is
-//                         located through a per-window row table built in LDS
-//                         from the closed-form plan (no materialised window
-//                         copies), its q/k RMSNorm * gamma, RoPE and bf16
-//                         rounding run in registers (RoPE cos/sin and gammas
-//                         staged in LDS per window), K and V^T tiles of 64
-//                         keys are double-buffered in LDS and three tiles'
-//                         global loads are in flight in registers while a
-//                         tile is consumed;  S^T = K Q^T on bf16 MFMA (exact operands),
-//                         online softmax in fp32 with lazy rescaling,
-//                         O^T += V^T P^T on fp16 MFMA;
-//                         ragged windows are handled by masking keys and
-//                         padding query rows; video outputs are written once
-//                         (the windows partition the grid), text outputs to
-//                         per-window bf16 partials;
+//                         one 12-wave workgroup per (window, head) and up to
+//                         384 query rows (windows with more rows split them
+//                         evenly over several workgroups).  Every video row of
+//                         the window is located through a per-window row table
+//                         built in LDS from the closed-form plan (no
+//                         materialised window copies).  Key/value tiles of 64
+//                         keys are fetched by waves 0-7 straight from global
+//                         memory into LDS (global_load_lds, no staging
+//                         registers), two tiles ahead; the same waves then run
+//                         the k prologue (RMSNorm * gamma, RoPE, bf16) in
+//                         place on the tile and write v, rounded to bf16 and
+//                         held as fp16, transposed.  Each wave owns 32 query
+//                         rows whose q prologue runs in registers.
+//                         S^T = K Q^T on bf16 MFMA (exact operands), online
+//                         softmax per 32-key subtile in fp32 with lazy
+//                         rescaling, O^T += V^T P^T on fp16 MFMA.  Ragged
+//                         windows: keys past the window are masked, query rows
+//                         past it are not stored.  Video outputs are written
+//                         once (the windows partition the grid), text outputs
+//                         to per-window bf16 partials;
 //   text_window_reduce_kernel
 //                         text outputs: partials summed in window order, times
 //                         1/nW, as the reference accumulates them.
@@ -44,36 +48,43 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;   // 512
-constexpr int kRowsPerGroup = kWaves * 32; // query rows per workgroup
-constexpr int kBlockN = 64;             // keys per tile (two 32x32 S^T subtiles)
-constexpr int kKStride = 136;           // halfs per LDS row of the key tile (128 + 8 pad)
-constexpr int kVtStride = 64;           // halfs per LDS row of the transposed value tile (swizzled)
-constexpr int kTextPad = 64;            // text rows of the prepared workspace are padded to this
-constexpr int kMaxVideoRows = 4096;     // video tokens per window the row table holds
-constexpr int kPrepRows = 16;           // text rows per text_prepare workgroup
-constexpr int kMaxRopeRows = 160;       // RoPE rows (t + y + x positions) of one window staged in LDS
-constexpr float kRescaleLog2 = 8.f;     // O is rescaled only when a row max grows by more than 2^8
-constexpr float kLog2e = 1.4426950408889634f;
-// s_waitcnt immediate for vmcnt(0) with expcnt / lgkmcnt left unconstrained
-// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
+constexpr int kWaves = 12;
+constexpr int kThreads = kWaves * 64;        // 768
+constexpr int kLoaderThreads = 512;          // waves 0-7 fetch and prepare key/value tiles
+constexpr int kRowsPerGroup = kWaves * 32;   // query rows per workgroup
+constexpr int kBlockN = 64;                  // keys per tile
+constexpr int kTileBytes = kBlockN * kHeadDim * 2; // one K, V or V^T tile of 16-bit values
+constexpr int kVtStride = 64;                // halfs per row of the transposed value tile (swizzled)
+constexpr int kTextPad = 64;                 // text rows of the prepared workspace are padded to this
+constexpr int kMaxVideoRows = 4096;          // video tokens per window (local coordinates fit 10 bits)
+constexpr int kPrepRows = 16;                // text rows per text_prepare workgroup
+constexpr int kMaxLds = 160 * 1024;          // LDS of one gfx950 CU
+// s_waitcnt immediates for vmcnt(0) / vmcnt(4) with expcnt and lgkmcnt left
+// unconstrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] << 14).  Each loader lane issues exactly four fetches per tile.
 constexpr int kWaitVmcnt0 = 0x0F70;
+constexpr int kWaitVmcnt4 = 0x0F74;
+constexpr float kRescaleLog2 = 8.f;          // O is rescaled only when a row max grows by more than 2^8
+constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- element types
 
 struct F32
 {
     static constexpr int kVec = 2; // uint4 per 8 elements
+    static constexpr bool kDma = false;
 };
 struct F16
 {
     static constexpr int kVec = 1;
+    static constexpr bool kDma = true;
 };
 struct BF16
 {
     static constexpr int kVec = 1;
+    static constexpr bool kDma = true;
 };
 
 template <typename T>
@@ -89,14 +100,6 @@ __device__ inline void load_raw8(const void* base, long long offset, uint4 (&r)[
     {
         r[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + offset);
     }
-}
-
-template <typename T>
-__device__ inline void zero_raw8(uint4 (&r)[T::kVec])
-{
-#pragma unroll
-    for (int i = 0; i < T::kVec; i++)
-        r[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 template <typename T>
@@ -214,9 +217,22 @@ __device__ inline void store2<BF16>(void* base, long long offset, float a, float
 
 // ---------------------------------------------------------------- parameters
 
+// Byte offsets of the dynamic LDS regions of one workgroup.
+struct LdsLayout
+{
+    int k;       // [3][64 rows][16 slots] x 16 B: key tiles, swizzled; bf16 after the prologue
+    int vraw;    // [2] x 16 KB: raw value tiles (video: [64 keys][16 chunks]; text: V^T slots)
+    int vt;      // [2][128 rows][64 keys] fp16: transposed value tiles, swizzled
+    int rows;    // int2 [vmax]: global video row, packed local (t | y << 10 | x << 20)
+    int rope;    // float2 [rope_rows][24]: cos/sin rows t..., y..., x... of the window
+    int gamma;   // float [2][128]: q, k gammas of the video branch
+    int total;
+};
+
 struct AttnParams
 {
     PlanArgs plan;
+    LdsLayout lds;
     const void* vid_qkv;
     const void* txt_qkv;
     long long row_stride; // elements per qkv row (3*D)
@@ -227,8 +243,8 @@ struct AttnParams
     int npairs;           // windows * heads
     int nqb;              // query blocks per (window, head)
     int qk_norm;
-    int rope_mode;
     int rope_npos;
+    int out_dtype;
     float eps;
     float score_log2;     // (1/sqrt(128)) * log2(e): exp(s*scale - m) = exp2(s*score_log2 - m')
     const float* gq_vid;
@@ -286,9 +302,10 @@ __device__ inline float partner_sum(float v)
 // RoPE axis and table slot of an even head dim.  Dims a variant leaves
 // unrotated (126, 127 of the reference layout) read slot 23, which the table
 // fills with (cos, sin) = (1, 0).
-__device__ inline void rope_axis_slot(int mode, int d, int* axis, int* slot)
+template <int RM>
+__device__ inline void rope_axis_slot(int d, int* axis, int* slot)
 {
-    if (mode == SV2_ROPE_ABSOLUTE)
+    if constexpr (RM == SV2_ROPE_ABSOLUTE)
     {
         if (d < 32)
         {
@@ -305,18 +322,20 @@ __device__ inline void rope_axis_slot(int mode, int d, int* axis, int* slot)
             *axis = 2;
             *slot = (d - 80) >> 1;
         }
-        return;
-    }
-    if (d < 126)
-    {
-        const int a = d / 42;
-        *axis = a;
-        *slot = (d - 42 * a) >> 1;
     }
     else
     {
-        *axis = 2;
-        *slot = kRopePairSlots - 1;
+        if (d < 126)
+        {
+            const int a = d / 42;
+            *axis = a;
+            *slot = (d - 42 * a) >> 1;
+        }
+        else
+        {
+            *axis = 2;
+            *slot = kRopePairSlots - 1;
+        }
     }
 }
 
@@ -326,20 +345,18 @@ __device__ inline float inv_rms(float ss, float eps)
 }
 
 // y = x * inv * gamma, then the rotation of the 4 adjacent pairs of the 8
-// dims (seedvr2_dit_block.cpp:950-971).  Multiplies and adds stay separate
-// (no contraction), as the reference evaluates them.  cs(q) gives the (cos,
-// sin) of pair q.
-template <typename CosSin>
-__device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, bool rotate, CosSin cs)
+// dims (seedvr2_dit_block.cpp:950-971): (a, b) -> (a c - b s, b c + a s).
+// cs(q) gives the (cos, sin) of pair q.
+template <bool kRotate, typename CosSin>
+__device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, CosSin cs)
 {
-#pragma clang fp contract(off)
     if (norm)
     {
 #pragma unroll
         for (int e = 0; e < 8; e++)
             x[e] = x[e] * inv * gamma8[e];
     }
-    if (rotate)
+    if constexpr (kRotate)
     {
 #pragma unroll
         for (int q = 0; q < 4; q++)
@@ -347,33 +364,10 @@ __device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv,
             const float2 c = cs(q);
             const float first = x[2 * q];
             const float second = x[2 * q + 1];
-            const float a = first * c.x;
-            const float b = second * c.y;
-            const float cc = second * c.x;
-            const float d = first * c.y;
-            x[2 * q] = a - b;
-            x[2 * q + 1] = cc + d;
+            x[2 * q] = __builtin_fmaf(first, c.x, -(second * c.y));
+            x[2 * q + 1] = __builtin_fmaf(second, c.x, first * c.y);
         }
     }
-}
-
-// Prologue of 8 dims of a row whose 128 dims are spread over 16 consecutive
-// lanes (all active): per-head RMSNorm (fp32 sum of squares), gamma, RoPE,
-// bf16 rounding.
-template <typename CosSin>
-__device__ inline uint4 prologue16(float x[8], const float* gamma8, bool rotate, CosSin cs, const AttnParams& p)
-{
-    float inv = 1.f;
-    if (p.qk_norm)
-    {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            ss = __builtin_fmaf(x[e], x[e], ss);
-        inv = inv_rms(row16_sum(ss), p.eps);
-    }
-    scale_rotate8(x, gamma8, inv, p.qk_norm != 0, rotate, cs);
-    return to_bf16x8(x);
 }
 
 // ---------------------------------------------------------------- layout helpers
@@ -385,6 +379,14 @@ __device__ inline uint4 prologue16(float x[8], const float* gamma8, bool rotate,
 __device__ inline int key_perm(int i)
 {
     return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+// Byte offset of chunk c (dims 8c..8c+7) of row r in a key tile: 16-byte
+// slots, XOR-swizzled so the MFMA operand reads of 16 rows hit 16 different
+// slot positions.
+__device__ inline int k_slot_offset(int r, int c)
+{
+    return (r * 16 + (c ^ (r & 15))) * 16;
 }
 
 // Swizzled offset (in halfs) of key group `grp` (8 keys, 0..7) in row d of the
@@ -408,14 +410,22 @@ __device__ inline f16x2 bf16_pair_as_f16(float a, float b)
                                                                 __builtin_bit_cast(float, u & 0xffff0000u)));
 }
 
-// ---------------------------------------------------------------- per-window staging
-
-struct WindowLds
+// A copy of v the compiler cannot see through.  Lane-derived offsets computed
+// from it inside the tile loop are recomputed each iteration (two or three
+// integer ops each) instead of being hoisted and kept live across the loop,
+// which would exceed the 168 VGPRs a 12-wave workgroup allows.
+__device__ inline int opaque(int v)
 {
-    int2 vrows[kMaxVideoRows];                    // global row, local (t | y<<10 | x<<20)
-    float2 rope[kMaxRopeRows * kRopePairSlots];   // rows t..., y..., x... of the window
-    float gamma[2][kHeadDim];                     // q, k gammas of the video branch
-};
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ inline void dma16(const void* g, char* lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
+
+// ---------------------------------------------------------------- per-window staging
 
 // Row of the staged RoPE table where each axis starts.
 struct RopeBase
@@ -432,22 +442,42 @@ __device__ inline RopeBase rope_base(const WindowBox& box)
     return r;
 }
 
+struct Staged
+{
+    const int2* rows;
+    const float2* rope;
+    const float* gamma;
+};
+
+__device__ inline Staged staged(const AttnParams& p, const char* smem)
+{
+    Staged s;
+    s.rows = reinterpret_cast<const int2*>(smem + p.lds.rows);
+    s.rope = reinterpret_cast<const float2*>(smem + p.lds.rope);
+    s.gamma = reinterpret_cast<const float*>(smem + p.lds.gamma);
+    return s;
+}
+
 // Fills the gather table, the window's RoPE rows and the gammas (threads
 // stride by nthreads; the caller synchronises).
-__device__ inline void stage_window(const AttnParams& p, const WindowBox& box, WindowLds& s, int tid, int nthreads)
+template <int RM>
+__device__ inline void stage_window(const AttnParams& p, const WindowBox& box, char* smem, int tid, int nthreads)
 {
+    int2* rows = reinterpret_cast<int2*>(smem + p.lds.rows);
+    float2* rope = reinterpret_cast<float2*>(smem + p.lds.rope);
+    float* gamma = reinterpret_cast<float*>(smem + p.lds.gamma);
     for (int j = tid; j < box.vlen; j += nthreads)
     {
         int lt, ly, lx;
         const int row = window_video_row(p.plan, box, j, &lt, &ly, &lx);
-        s.vrows[j] = make_int2(row, static_cast<int>(static_cast<uint32_t>(lt) | (static_cast<uint32_t>(ly) << 10) |
-                                                     (static_cast<uint32_t>(lx) << 20)));
+        rows[j] = make_int2(row, static_cast<int>(static_cast<uint32_t>(lt) | (static_cast<uint32_t>(ly) << 10) |
+                                                  (static_cast<uint32_t>(lx) << 20)));
     }
-    if (p.rope_mode != SV2_ROPE_NONE)
+    if constexpr (RM != SV2_ROPE_NONE)
     {
-        const int rows = box.lt + box.lh + box.lw;
-        const bool ref = p.rope_mode == SV2_ROPE_REFERENCE;
-        for (int i = tid; i < rows * kRopePairSlots; i += nthreads)
+        const int nrows = box.lt + box.lh + box.lw;
+        constexpr bool ref = RM == SV2_ROPE_REFERENCE;
+        for (int i = tid; i < nrows * kRopePairSlots; i += nthreads)
         {
             const int r = i / kRopePairSlots;
             const int slot = i - r * kRopePairSlots;
@@ -467,50 +497,75 @@ __device__ inline void stage_window(const AttnParams& p, const WindowBox& box, W
                 axis = 2;
                 gpos = (r - box.lt - box.lh) + (ref ? 0 : box.w0);
             }
-            s.rope[i] = p.rope_tab[(axis * p.rope_npos + gpos) * kRopePairSlots + slot];
+            rope[i] = p.rope_tab[(axis * p.rope_npos + gpos) * kRopePairSlots + slot];
         }
     }
     for (int i = tid; i < 2 * kHeadDim; i += nthreads)
     {
         const float* src = i < kHeadDim ? p.gq_vid : p.gk_vid;
-        s.gamma[i / kHeadDim][i % kHeadDim] = p.qk_norm ? src[i % kHeadDim] : 1.f;
+        gamma[i] = p.qk_norm ? src[i % kHeadDim] : 1.f;
     }
 }
 
 // Query operand of S^T = K Q^T for window-sequence row qrow (clamped by the
-// caller to a valid row): lane holds dims 16c + 8g .. +7 of the row, the
-// partner lane (lane ^ 32) the other half.  Video rows run the prologue here;
-// text rows read the prepared workspace.
+// caller to a valid row): the lane holds dims 16c + 8g .. +7 of the row, the
+// partner lane (lane ^ 32) the other half.  Video rows: the raw row is loaded
+// by query_load and its prologue runs in query_finish; text rows read the
+// prepared workspace.
 template <typename TI>
-__device__ inline void query_operand(const AttnParams& p, const WindowBox& box, const WindowLds& s, int head,
-                                     int qrow, int g, bf16x8 qf[8])
+struct QueryRaw
 {
-    const bool is_video = qrow < box.vlen;
-    const long long q_col = static_cast<long long>(head) * kHeadDim;
-    if (!is_video)
+    uint4 r[8][TI::kVec];
+};
+
+template <typename TI>
+__device__ inline void query_load(const AttnParams& p, const Staged& s, const WindowBox& box, int head, int qrow,
+                                  int g, QueryRaw<TI>& raw)
+{
+    if (qrow < box.vlen)
     {
-        const uint16_t* src = p.txt_q + (static_cast<long long>(head) * p.text_len + (qrow - box.vlen)) * kHeadDim;
+        const long long base = static_cast<long long>(s.rows[qrow].x) * p.row_stride +
+                               static_cast<long long>(head) * kHeadDim + 8 * g;
 #pragma unroll
         for (int c = 0; c < 8; c++)
-            qf[c] = *reinterpret_cast<const bf16x8*>(src + 16 * c + 8 * g);
+            load_raw8<TI>(p.vid_qkv, base + 16 * c, raw.r[c]);
+    }
+    else
+    {
+        const uint16_t* src = p.txt_q + (static_cast<long long>(head) * p.text_len + (qrow - box.vlen)) * kHeadDim + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+        {
+            raw.r[c][0] = *reinterpret_cast<const uint4*>(src + 16 * c);
+            if constexpr (TI::kVec == 2)
+                raw.r[c][1] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+template <typename TI, int RM>
+__device__ inline void query_finish(const AttnParams& p, const Staged& s, const WindowBox& box, int qrow, int g,
+                                    const QueryRaw<TI>& raw, bf16x8 qf[8])
+{
+    const bool is_video = qrow < box.vlen;
+    if (!is_video)
+    {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            qf[c] = __builtin_bit_cast(bf16x8, raw.r[c][0]);
     }
     // both lanes of a pair take the same branch; the partner exchange below
     // runs on every lane
     float x[64];
-    uint32_t packed = 0u;
-    if (is_video)
-    {
-        const int2 vr = s.vrows[qrow];
-        packed = static_cast<uint32_t>(vr.y);
 #pragma unroll
-        for (int c = 0; c < 8; c++)
-            load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 16 * c + 8 * g, &x[8 * c]);
-    }
-    else
+    for (int c = 0; c < 8; c++)
     {
+        if (is_video)
+            raw8_to_float<TI>(raw.r[c], &x[8 * c]);
+        else
 #pragma unroll
-        for (int i = 0; i < 64; i++)
-            x[i] = 0.f;
+            for (int e = 0; e < 8; e++)
+                x[8 * c + e] = 0.f;
     }
     float inv = 1.f;
     if (p.qk_norm)
@@ -523,17 +578,18 @@ __device__ inline void query_operand(const AttnParams& p, const WindowBox& box, 
     }
     if (!is_video)
         return;
+    const uint32_t packed = static_cast<uint32_t>(s.rows[qrow].y);
     const RopeBase rb = rope_base(box);
-    const bool rotate = p.rope_mode != SV2_ROPE_NONE;
 #pragma unroll
     for (int c = 0; c < 8; c++)
     {
         const int d0 = 16 * c + 8 * g;
-        scale_rotate8(&x[8 * c], &s.gamma[0][d0], inv, p.qk_norm != 0, rotate, [&](int q) {
+        scale_rotate8<RM != SV2_ROPE_NONE>(&x[8 * c], &s.gamma[d0], inv, p.qk_norm != 0, [&](int q) {
             int axis, slot;
-            rope_axis_slot(p.rope_mode, d0 + 2 * q, &axis, &slot);
+            rope_axis_slot<RM>(d0 + 2 * q, &axis, &slot);
             const int local = static_cast<int>((packed >> (10 * axis)) & 1023u);
-            return s.rope[(rb.b[axis] + local) * kRopePairSlots + slot];
+            const int row0 = axis == 0 ? rb.b[0] : (axis == 1 ? rb.b[1] : rb.b[2]);
+            return s.rope[(row0 + local) * kRopePairSlots + slot];
         });
         qf[c] = __builtin_bit_cast(bf16x8, to_bf16x8(&x[8 * c]));
     }
@@ -548,28 +604,45 @@ struct KeyRope
     int shift[4];
 };
 
-__device__ inline KeyRope key_rope(const AttnParams& p, const RopeBase& rb, int d0)
+template <int RM>
+__device__ inline KeyRope key_rope(const RopeBase& rb, int d0)
 {
     KeyRope k;
 #pragma unroll
     for (int q = 0; q < 4; q++)
     {
         int axis, slot;
-        rope_axis_slot(p.rope_mode, d0 + 2 * q, &axis, &slot);
-        k.off[q] = rb.b[axis] * kRopePairSlots + slot;
+        rope_axis_slot<RM>(d0 + 2 * q, &axis, &slot);
+        // selects rather than rb.b[axis]: a runtime index would put the
+        // array in scratch memory
+        const int row0 = axis == 0 ? rb.b[0] : (axis == 1 ? rb.b[1] : rb.b[2]);
+        k.off[q] = row0 * kRopePairSlots + slot;
         k.shift[q] = 10 * axis;
     }
     return k;
 }
 
-// Prologue of one key chunk (8 dims of the row with packed local positions).
-__device__ inline uint4 key_chunk(const AttnParams& p, const WindowLds& s, const KeyRope& kr, float x[8], int d0,
+// Prologue of one key chunk (8 dims of a row whose 128 dims are spread over
+// 16 consecutive lanes, all active): per-head RMSNorm (fp32 sum of squares),
+// gamma, RoPE, bf16 rounding.
+template <int RM>
+__device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const KeyRope& kr, float x[8], int d0,
                                   uint32_t packed)
 {
-    return prologue16(x, &s.gamma[1][d0], p.rope_mode != SV2_ROPE_NONE, [&](int q) {
+    float inv = 1.f;
+    if (p.qk_norm)
+    {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            ss = __builtin_fmaf(x[e], x[e], ss);
+        inv = inv_rms(row16_sum(ss), p.eps);
+    }
+    scale_rotate8<RM != SV2_ROPE_NONE>(x, &s.gamma[kHeadDim + d0], inv, p.qk_norm != 0, [&](int q) {
         const int local = static_cast<int>((packed >> kr.shift[q]) & 1023u);
         return s.rope[kr.off[q] + local * kRopePairSlots];
-    }, p);
+    });
+    return to_bf16x8(x);
 }
 
 // ---------------------------------------------------------------- text prepare
@@ -578,7 +651,7 @@ __device__ inline uint4 key_chunk(const AttnParams& p, const WindowLds& s, const
 // (l, l, l) in the reference RoPE mode (text is not rotated in the absolute
 // mode), v rounded to bf16 and stored as fp16, transposed; zero padding up to
 // text_pad so masked keys multiply finite values.
-template <typename TI>
+template <typename TI, int RM>
 __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
 {
     const int head = blockIdx.y;
@@ -596,11 +669,10 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
         load8<TI>(p.txt_qkv, row + p.dim + d0, k);
         load8<TI>(p.txt_qkv, row + 2LL * p.dim + d0, v);
     }
-    const bool rotate = p.rope_mode == SV2_ROPE_REFERENCE;
     const int pos = valid ? l : 0;
     auto cs = [&](int qq) {
         int axis, slot;
-        rope_axis_slot(p.rope_mode, d0 + 2 * qq, &axis, &slot);
+        rope_axis_slot<RM>(d0 + 2 * qq, &axis, &slot);
         return p.rope_tab[(axis * p.rope_npos + pos) * kRopePairSlots + slot];
     };
     float gq[8];
@@ -611,8 +683,26 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
         gq[e] = p.qk_norm ? p.gq_txt[d0 + e] : 1.f;
         gk[e] = p.qk_norm ? p.gk_txt[d0 + e] : 1.f;
     }
-    const uint4 qb = prologue16(q, gq, rotate, cs, p);
-    const uint4 kb = prologue16(k, gk, rotate, cs, p);
+    float iq = 1.f;
+    float ik = 1.f;
+    if (p.qk_norm)
+    {
+        float sq = 0.f;
+        float sk = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            sq = __builtin_fmaf(q[e], q[e], sq);
+            sk = __builtin_fmaf(k[e], k[e], sk);
+        }
+        iq = inv_rms(row16_sum(sq), p.eps);
+        ik = inv_rms(row16_sum(sk), p.eps);
+    }
+    constexpr bool rotate = RM == SV2_ROPE_REFERENCE;
+    scale_rotate8<rotate>(q, gq, iq, p.qk_norm != 0, cs);
+    scale_rotate8<rotate>(k, gk, ik, p.qk_norm != 0, cs);
+    const uint4 qb = to_bf16x8(q);
+    const uint4 kb = to_bf16x8(k);
     if (l >= p.text_pad)
         return;
     if (valid)
@@ -632,23 +722,7 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
     }
 }
 
-// ---------------------------------------------------------------- main kernel
-
-// Registers holding one tile between its global loads and its LDS store.
-// Video tiles: every thread holds two key items (rows r and r+32 of the tile,
-// the same 8 dims) in k0/k1 and one value item (keys 2kp and 2kp+1, 8 dims)
-// in v0/v1.  Text tiles (prepared data): k0/k1 hold key rows r and r+32, v0/v1
-// the value items tid and tid+512 (row of V^T, group of 8 keys).
-template <typename TI>
-struct TileRegs
-{
-    uint4 k0[TI::kVec];
-    uint4 k1[TI::kVec];
-    uint4 v0[TI::kVec];
-    uint4 v1[TI::kVec];
-    uint32_t pk0;
-    uint32_t pk1;
-};
+// ---------------------------------------------------------------- key/value tiles
 
 struct Geometry
 {
@@ -658,124 +732,239 @@ struct Geometry
     int nkb;    // all key tiles
 };
 
-// Issues the global loads of key tile kb into registers.  Rows past the end
-// of a ragged tile are clamped to the last valid row: their scores are masked
-// and their values multiply p = 0, so any finite data will do.
-template <typename TI>
-__device__ inline void load_tile(const AttnParams& p, const Geometry& gm, const WindowLds& s, int head, int kb,
-                                 int tid, TileRegs<TI>& t)
+__device__ inline char* k_tile(char* smem, const AttnParams& p, int kb)
 {
-    const int r = tid >> 4;
-    const int chunk = tid & 15;
+    return smem + p.lds.k + (kb % 3) * kTileBytes;
+}
+
+__device__ inline char* vraw_tile(char* smem, const AttnParams& p, int kb)
+{
+    return smem + p.lds.vraw + (kb & 1) * kTileBytes;
+}
+
+__device__ inline char* vt_tile(char* smem, const AttnParams& p, int kb)
+{
+    return smem + p.lds.vt + (kb & 1) * kTileBytes;
+}
+
+// 16-bit inputs: waves 0-7 move tile kb from global memory straight into LDS,
+// four 1 KB wave-instructions per wave (the lane order fixes where each
+// 16-byte chunk lands).  Wave w fetches key rows 4w..4w+3 and 32+4w..32+4w+3
+// of the key tile (swizzled) and value rows 8w..8w+7 — exactly the rows it
+// prepares afterwards, so no barrier separates the fetch from the prologue.
+// Rows past the end of a ragged tile repeat the last valid row: their scores
+// are masked and their values multiply p = 0.
+template <typename TI>
+__device__ inline void dma_tile(const AttnParams& p, const Geometry& gm, const Staged& s, char* smem, int head,
+                                int kb, int wave, int lane)
+{
+    char* kt = k_tile(smem, p, kb);
+    char* vr = vraw_tile(smem, p, kb);
+    const int sub = lane >> 4;
+    const int slot = lane & 15;
     if (kb < gm.ntb)
     {
         const int base = kb * kBlockN;
         const long long kbase = static_cast<long long>(head) * p.text_len;
-        const int l0 = min(base + r, p.text_len - 1);
-        const int l1 = min(base + r + 32, p.text_len - 1);
-        t.k0[0] = *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l0) * kHeadDim + chunk * 8);
-        t.k1[0] = *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l1) * kHeadDim + chunk * 8);
-        const long long vbase = static_cast<long long>(head) * kHeadDim;
-        const int i0 = tid;
-        const int i1 = tid + kThreads;
-        t.v0[0] = *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (i0 >> 3)) * p.text_pad + base + (i0 & 7) * 8);
-        t.v1[0] = *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (i1 >> 3)) * p.text_pad + base + (i1 & 7) * 8);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+        {
+            const int r = 32 * i + 4 * wave + sub;
+            const int l = min(base + r, p.text_len - 1);
+            const int c = slot ^ (r & 15);
+            dma16(p.txt_k + (kbase + l) * kHeadDim + 8 * c, kt + (32 * i + 4 * wave) * 256);
+        }
+        // V^T slots: instruction q covers rows d = 8q .. 8q+7 of the transposed tile
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+        {
+            const int q = 2 * wave + i;
+            const int d = 8 * q + (lane >> 3);
+            const int sl = lane & 7;
+            const int grp = sl ^ ((d ^ (d >> 3)) & 7);
+            dma16(p.txt_vt + (static_cast<long long>(head) * kHeadDim + d) * p.text_pad + base + 8 * grp,
+                  vr + q * 1024);
+        }
         return;
     }
     const int base = (kb - gm.ntb) * kBlockN;
-    const long long k_col = static_cast<long long>(p.dim) + static_cast<long long>(head) * kHeadDim + chunk * 8;
-    const long long v_col = k_col + p.dim;
     const int last = gm.vlen - 1;
-    const int2 a = s.vrows[min(base + r, last)];
-    const int2 b = s.vrows[min(base + r + 32, last)];
-    t.pk0 = static_cast<uint32_t>(a.y);
-    t.pk1 = static_cast<uint32_t>(b.y);
-    load_raw8<TI>(p.vid_qkv, static_cast<long long>(a.x) * p.row_stride + k_col, t.k0);
-    load_raw8<TI>(p.vid_qkv, static_cast<long long>(b.x) * p.row_stride + k_col, t.k1);
-    const int j0 = base + 2 * r; // key pair of this thread's value item
-    const int r0 = s.vrows[min(j0, last)].x;
-    const int r1 = s.vrows[min(j0 + 1, last)].x;
-    load_raw8<TI>(p.vid_qkv, static_cast<long long>(r0) * p.row_stride + v_col, t.v0);
-    load_raw8<TI>(p.vid_qkv, static_cast<long long>(r1) * p.row_stride + v_col, t.v1);
+    const long long k_col = static_cast<long long>(p.dim) + static_cast<long long>(head) * kHeadDim;
+    const long long v_col = k_col + p.dim;
+    const uint16_t* src = static_cast<const uint16_t*>(p.vid_qkv);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+    {
+        const int r = 32 * i + 4 * wave + sub;
+        const int c = slot ^ (r & 15);
+        const int row = s.rows[min(base + r, last)].x;
+        dma16(src + static_cast<long long>(row) * p.row_stride + k_col + 8 * c, kt + (32 * i + 4 * wave) * 256);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+    {
+        const int r = 8 * wave + 4 * i + sub;
+        const int row = s.rows[min(base + r, last)].x;
+        dma16(src + static_cast<long long>(row) * p.row_stride + v_col + 8 * slot, vr + (8 * wave + 4 * i) * 256);
+    }
 }
 
-// Runs the prologue on the registers of tile kb and writes them to LDS.
-template <typename TI>
-__device__ inline void store_tile(const AttnParams& p, const Geometry& gm, const WindowLds& s, const KeyRope& kr,
-                                  int kb, int tid, const TileRegs<TI>& t, uint16_t* k_tile, uint16_t* vt_tile)
+// Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0).
+__device__ inline void store_vt_pair(char* vt, int r, int d0, const float v0[8], const float v1[8])
 {
-    const int r = tid >> 4;
-    const int d0 = (tid & 15) * 8;
+    uint16_t* t = reinterpret_cast<uint16_t*>(vt);
+    const int key = 2 * r;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        *reinterpret_cast<f16x2*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = bf16_pair_as_f16(v0[e], v1[e]);
+}
+
+// 16-bit inputs: the prologue of tile kb, run by the wave that fetched it
+// (after its own fetch has landed).  Video: k in place (RMSNorm * gamma, RoPE,
+// bf16), v rounded to bf16 and transposed into the V^T tile.  Text (prepared
+// in the workspace): the V^T slots are copied to the V^T tile.
+template <typename TI, int RM>
+__device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, const Staged& s, const RopeBase& rb,
+                                    char* smem, int kb, int wave, int lane)
+{
+    char* vt = vt_tile(smem, p, kb);
+    const char* vr = vraw_tile(smem, p, kb);
     if (kb < gm.ntb)
     {
-        *reinterpret_cast<uint4*>(&k_tile[r * kKStride + d0]) = t.k0[0];
-        *reinterpret_cast<uint4*>(&k_tile[(r + 32) * kKStride + d0]) = t.k1[0];
-        const int i0 = tid;
-        const int i1 = tid + kThreads;
-        *reinterpret_cast<uint4*>(&vt_tile[vt_offset(i0 >> 3, i0 & 7)]) = t.v0[0];
-        *reinterpret_cast<uint4*>(&vt_tile[vt_offset(i1 >> 3, i1 & 7)]) = t.v1[0];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+        {
+            const int off = (2 * wave + i) * 1024 + lane * 16;
+            *reinterpret_cast<uint4*>(vt + off) = *reinterpret_cast<const uint4*>(vr + off);
+        }
         return;
     }
+    char* kt = k_tile(smem, p, kb);
+    const int base = (kb - gm.ntb) * kBlockN;
+    const int last = gm.vlen - 1;
+    const int chunk = lane & 15;
+    const int d0 = chunk * 8;
+    const KeyRope kr = key_rope<RM>(rb, d0);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
     {
+        const int r = 32 * i + 4 * wave + (lane >> 4);
+        uint4* slot = reinterpret_cast<uint4*>(kt + k_slot_offset(r, chunk));
+        uint4 raw[1] = {*slot};
         float x[8];
-        raw8_to_float<TI>(t.k0, x);
-        *reinterpret_cast<uint4*>(&k_tile[r * kKStride + d0]) = key_chunk(p, s, kr, x, d0, t.pk0);
+        raw8_to_float<TI>(raw, x);
+        const uint32_t packed = static_cast<uint32_t>(s.rows[min(base + r, last)].y);
+        *slot = key_chunk<RM>(p, s, kr, x, d0, packed);
     }
     {
-        float x[8];
-        raw8_to_float<TI>(t.k1, x);
-        *reinterpret_cast<uint4*>(&k_tile[(r + 32) * kKStride + d0]) = key_chunk(p, s, kr, x, d0, t.pk1);
-    }
-    {
-        const int key = 2 * r;
+        const int r = 4 * wave + (lane >> 4); // keys 2r, 2r+1 = rows 8w + 2 (lane >> 4) (+1) of the raw tile
+        uint4 a[1] = {*reinterpret_cast<const uint4*>(vr + ((2 * r) * 16 + chunk) * 16)};
+        uint4 b[1] = {*reinterpret_cast<const uint4*>(vr + ((2 * r + 1) * 16 + chunk) * 16)};
         float v0[8];
         float v1[8];
-        raw8_to_float<TI>(t.v0, v0);
-        raw8_to_float<TI>(t.v1, v1);
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            *reinterpret_cast<f16x2*>(&vt_tile[vt_offset(d0 + e, key >> 3) + (key & 7)]) = bf16_pair_as_f16(v0[e], v1[e]);
+        raw8_to_float<TI>(a, v0);
+        raw8_to_float<TI>(b, v1);
+        store_vt_pair(vt, r, d0, v0, v1);
     }
 }
 
-// One 64-key tile of the online softmax for the wave's 32 query rows.
-__device__ inline void attend_tile(const AttnParams& p, const uint16_t* kt_base, const uint16_t* vt_base,
-                                   const bf16x8 qf[8], int nvalid, int lr, int g, f32x16 o[4], float& m_run,
-                                   float& l_run)
+// fp32 inputs: waves 0-7 load tile kb into registers and prepare it into the
+// same LDS tiles (no raw copy in LDS).
+template <int RM>
+__device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry& gm, const Staged& s,
+                                             const RopeBase& rb, char* smem, int head, int kb, int tid)
 {
-    // ---- S^T for two 32-key subtiles
-    f32x16 s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+    char* kt = k_tile(smem, p, kb);
+    char* vt = vt_tile(smem, p, kb);
+    const int r = tid >> 4;
+    const int chunk = tid & 15;
+    const int d0 = chunk * 8;
+    const KeyRope kr = key_rope<RM>(rb, d0);
+    if (kb < gm.ntb)
     {
-        s[kt] = f32x16{};
-        const uint16_t* krow = kt_base + (kt * 32 + key_perm(lr)) * kKStride + 8 * g;
+        const int base = kb * kBlockN;
+        const long long kbase = static_cast<long long>(head) * p.text_len;
 #pragma unroll
-        for (int c = 0; c < 8; c++)
+        for (int i = 0; i < 2; i++)
         {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + 16 * c);
-            s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
+            const int rr = r + 32 * i;
+            const int l = min(base + rr, p.text_len - 1);
+            *reinterpret_cast<uint4*>(kt + k_slot_offset(rr, chunk)) =
+                *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l) * kHeadDim + d0);
         }
+        const long long vbase = static_cast<long long>(head) * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+        {
+            const int item = tid + kLoaderThreads * i; // row d = item >> 3, key group item & 7
+            *reinterpret_cast<uint4*>(vt + 2 * vt_offset(item >> 3, item & 7)) =
+                *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (item >> 3)) * p.text_pad + base + (item & 7) * 8);
+        }
+        return;
     }
-    // ---- mask ragged tiles, online softmax (row = this lane's query)
-    if (nvalid < kBlockN)
+    const int base = (kb - gm.ntb) * kBlockN;
+    const int last = gm.vlen - 1;
+    const long long k_col = static_cast<long long>(p.dim) + static_cast<long long>(head) * kHeadDim + d0;
+    const long long v_col = k_col + p.dim;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
     {
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-            {
-                const int key = kt * 32 + key_perm(8 * (r >> 2) + 4 * g + (r & 3));
-                if (key >= nvalid)
-                    s[kt][r] = -INFINITY;
-            }
+        const int rr = r + 32 * i;
+        const int2 a = s.rows[min(base + rr, last)];
+        float x[8];
+        load8<F32>(p.vid_qkv, static_cast<long long>(a.x) * p.row_stride + k_col, x);
+        *reinterpret_cast<uint4*>(kt + k_slot_offset(rr, chunk)) =
+            key_chunk<RM>(p, s, kr, x, d0, static_cast<uint32_t>(a.y));
     }
-    float smax = s[0][0];
+    float v0[8];
+    float v1[8];
+    load8<F32>(p.vid_qkv, static_cast<long long>(s.rows[min(base + 2 * r, last)].x) * p.row_stride + v_col, v0);
+    load8<F32>(p.vid_qkv, static_cast<long long>(s.rows[min(base + 2 * r + 1, last)].x) * p.row_stride + v_col, v1);
+    store_vt_pair(vt, r, d0, v0, v1);
+}
+
+// ---------------------------------------------------------------- attention step
+
+// One 32-key subtile of the online softmax for the wave's 32 query rows.
+__device__ inline void attend_subtile(const AttnParams& p, const char* kt, const uint16_t* vt, int kt_idx,
+                                      const bf16x8 qf[8], int nvalid, int lane, f32x16 o[4], float& m_run,
+                                      float& l_run)
+{
+    const int lr = lane & 31;
+    const int g = lane >> 5;
+    // ---- S^T = K Q^T for 32 keys; K fragments are read four at a time ahead
+    // of the MFMAs that consume them
+    const int row = kt_idx * 32 + key_perm(lr);
+    f32x16 s = f32x16{};
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+    for (int h = 0; h < 2; h++)
+    {
+        bf16x8 a[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            a[c] = *reinterpret_cast<const bf16x8*>(kt + k_slot_offset(row, 2 * (4 * h + c) + g));
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c], qf[4 * h + c], s, 0, 0, 0);
+    }
+    // ---- mask a ragged subtile.  Register r of lane group g holds S^T row
+    // 8(r/4) + 4g + r%4, i.e. key 16((r/4)/2) + 8g + 4((r/4)%2) + r%4; the
+    // per-register part is a constant, so only one limit is live.
+    if (nvalid < 32)
+    {
+        const int lim = nvalid - 8 * g;
 #pragma unroll
         for (int r = 0; r < 16; r++)
-            smax = fmaxf(smax, s[kt][r]);
+        {
+            const int kconst = 16 * ((r >> 2) >> 1) + 4 * ((r >> 2) & 1) + (r & 3);
+            if (kconst >= lim)
+                s[r] = -INFINITY;
+        }
+    }
+    float smax = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++)
+        smax = fmaxf(smax, s[r]);
     const float m_new = fmaxf(m_run, partner_max(smax));
     // lazy rescale: keep the old reference max unless it is exceeded by more
     // than 2^8 (p stays <= 256, exact in fp16 and fp32); O / l does not depend
@@ -796,37 +985,35 @@ __device__ inline void attend_tile(const AttnParams& p, const uint16_t* kt_base,
     const float bias = m_run * p.score_log2;
     // ---- P (fp16), row sums from the same fp16 values, O^T += V^T P^T
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+    for (int c2 = 0; c2 < 2; c2++)
+    {
+        const int kgrp = kt_idx * 4 + c2 * 2 + g;
+        f16x8 va[4];
 #pragma unroll
-        for (int c2 = 0; c2 < 2; c2++)
+        for (int dt = 0; dt < 4; dt++)
+            va[dt] = *reinterpret_cast<const f16x8*>(vt + vt_offset(dt * 32 + lr, kgrp));
+        f16x8 b;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
         {
-            f16x8 b;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2)
-            {
-                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * c2 + e], p.score_log2, -bias));
-                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * c2 + e + 1], p.score_log2, -bias));
-                f16x2 h;
-                h[0] = static_cast<_Float16>(p0); // round to nearest even (v_cvt_pk_f16_f32)
-                h[1] = static_cast<_Float16>(p1);
-                b[e] = h[0];
-                b[e + 1] = h[1];
-                l_run = __builtin_amdgcn_fdot2(h, f16x2{static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)}, l_run,
-                                               false);
-            }
-            const int kgrp = kt * 4 + c2 * 2 + g;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-            {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(vt_base + vt_offset(dt * 32 + lr, kgrp));
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[dt], 0, 0, 0);
-            }
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c2 + e], p.score_log2, -bias));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c2 + e + 1], p.score_log2, -bias));
+            f16x2 h;
+            h[0] = static_cast<_Float16>(p0); // round to nearest even (v_cvt_pk_f16_f32)
+            h[1] = static_cast<_Float16>(p1);
+            b[e] = h[0];
+            b[e + 1] = h[1];
+            l_run = __builtin_amdgcn_fdot2(h, f16x2{static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)}, l_run,
+                                           false);
         }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], b, o[dt], 0, 0, 0);
+    }
 }
 
 // Query rows of one workgroup: a window of S rows is split into
-// ceil(S / 256) blocks of equal size (rounded up to 32 rows), so a large
-// window keeps all its query waves busy.
+// ceil(S / 384) blocks of equal size (rounded up to 32 rows).
 struct QueryBlock
 {
     int q0;
@@ -843,111 +1030,17 @@ __device__ inline QueryBlock query_block(int seq, int qb)
     return b;
 }
 
-template <typename TI, typename TO>
-__global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p)
+template <typename TO>
+__device__ inline void write_outputs(const AttnParams& p, const Staged& s, const WindowBox& box, int wi, int head,
+                                     int qrow, int g, const f32x16 o[4], float inv_l)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t k_tiles[2][kBlockN * kKStride];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_tiles[2][kHeadDim * kVtStride];
-    __shared__ WindowLds lds;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    // XCD-aware decode: workgroup ids go round-robin over the 8 XCDs; the query
-    // blocks of one (window, head) pair are consecutive ids of one XCD, run
-    // side by side and share its L2 for the key/value rows they both read.
-    const int id = blockIdx.x;
-    const int xcd = id & 7;
-    const int slot = id >> 3;
-    const int grp = slot / p.nqb;
-    const int pair = grp * 8 + xcd;
-    const int qb = slot - grp * p.nqb;
-    if (pair >= p.npairs)
-        return;
-    const int wi = pair / p.heads;
-    const int head = pair - wi * p.heads;
-    const WindowBox box = window_box(p.plan, wi);
-    Geometry gm;
-    gm.vlen = box.vlen;
-    gm.seq = box.vlen + p.text_len;
-    gm.ntb = (p.text_len + kBlockN - 1) / kBlockN;
-    gm.nkb = gm.ntb + (box.vlen + kBlockN - 1) / kBlockN;
-    const QueryBlock qbk = query_block(gm.seq, qb);
-    if (qbk.q0 >= gm.seq)
-        return;
-
-    stage_window(p, box, lds, tid, kThreads);
-    __syncthreads();
-
-    const int lr = lane & 31;
-    const int g = lane >> 5;
-    const bool wave_active = qbk.q0 + wave * 32 < qbk.q1;
-    const int qrow = qbk.q0 + wave * 32 + lr;
-    const KeyRope kr = key_rope(p, rope_base(box), (tid & 15) * 8);
-
-    bf16x8 qf[8];
-    query_operand<TI>(p, box, lds, head, min(qrow, gm.seq - 1), g, qf);
-    // every query load completes here, before any tile load is issued: with
-    // nothing older pending, the waits the compiler places in front of the
-    // MFMAs that read qf do not drain the tile prefetches below
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-
-    // three tiles in flight: loads of tile kb+3 are issued while tile kb is
-    // consumed, into the registers tile kb occupied (stored two steps before).
-    // Every step issues its loads (past the last tile they repeat the last
-    // one, an L2 hit), so the number of loads in flight is the same on every
-    // path and each store waits only for the tile it stores.
-    const int last_tile = gm.nkb - 1;
-    TileRegs<TI> ra, rb, rc;
-    load_tile<TI>(p, gm, lds, head, 0, tid, ra);
-    load_tile<TI>(p, gm, lds, head, min(1, last_tile), tid, rb);
-    load_tile<TI>(p, gm, lds, head, min(2, last_tile), tid, rc);
-
-    f32x16 o[4];
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-        o[dt] = f32x16{};
-    float m_run = -INFINITY;
-    float l_run = 0.f;
-
-    store_tile<TI>(p, gm, lds, kr, 0, tid, ra, k_tiles[0], vt_tiles[0]);
-    __syncthreads();
-
-    auto valid_keys = [&](int kb) {
-        return kb < gm.ntb ? p.text_len - kb * kBlockN : gm.vlen - (kb - gm.ntb) * kBlockN;
-    };
-    // step kb: attend tile kb, store tile kb+1 from `next`, reload `cur`
-    // (which held tile kb) with tile kb+3
-    auto step = [&](int kb, TileRegs<TI>& cur, TileRegs<TI>& next) {
-        const int buf = kb & 1;
-        if (kb < gm.nkb && wave_active)
-            attend_tile(p, k_tiles[buf], vt_tiles[buf], qf, valid_keys(kb), lr, g, o, m_run, l_run);
-        if (kb + 1 < gm.nkb)
-            store_tile<TI>(p, gm, lds, kr, kb + 1, tid, next, k_tiles[buf ^ 1], vt_tiles[buf ^ 1]);
-        load_tile<TI>(p, gm, lds, head, min(kb + 3, last_tile), tid, cur);
-        __syncthreads();
-    };
-    for (int kb = 0; kb < gm.nkb; kb += 3)
-    {
-        step(kb, ra, rb);
-        step(kb + 1, rb, rc);
-        step(kb + 2, rc, ra);
-    }
-
-    if (!wave_active)
-        return;
-    const float l_tot = partner_sum(l_run);
-    if (qrow >= qbk.q1)
-        return;
-    const float inv_l = 1.f / l_tot;
     const long long q_col = static_cast<long long>(head) * kHeadDim;
-    const bool text = qrow >= gm.vlen;
+    const bool text = qrow >= box.vlen;
     long long out_off;
     if (!text)
-        out_off = static_cast<long long>(lds.vrows[qrow].x) * p.dim + q_col;
+        out_off = static_cast<long long>(s.rows[qrow].x) * p.dim + q_col;
     else
-        out_off = (static_cast<long long>(wi) * p.text_len + (qrow - gm.vlen)) * p.dim + q_col;
+        out_off = (static_cast<long long>(wi) * p.text_len + (qrow - box.vlen)) * p.dim + q_col;
     const long long pre_row =
         (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + qrow) * p.dim + q_col;
 #pragma unroll
@@ -971,6 +1064,143 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
             else
                 store4<BF16>(p.partial, out_off + d, rounded);
         }
+}
+
+template <typename TI, int RM>
+__global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p)
+{
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const bool loader = tid < kLoaderThreads;
+
+    // XCD-aware decode: workgroup ids go round-robin over the 8 XCDs; the query
+    // blocks of one (window, head) pair are consecutive ids of one XCD and
+    // share its L2 for the key/value rows they both read.
+    const int id = blockIdx.x;
+    const int xcd = id & 7;
+    const int slot = id >> 3;
+    const int grp = slot / p.nqb;
+    const int pair = grp * 8 + xcd;
+    const int qb = slot - grp * p.nqb;
+    if (pair >= p.npairs)
+        return;
+    const int wi = pair / p.heads;
+    const int head = pair - wi * p.heads;
+    const WindowBox box = window_box(p.plan, wi);
+    Geometry gm;
+    gm.vlen = box.vlen;
+    gm.seq = box.vlen + p.text_len;
+    gm.ntb = (p.text_len + kBlockN - 1) / kBlockN;
+    gm.nkb = gm.ntb + (box.vlen + kBlockN - 1) / kBlockN;
+    const QueryBlock qbk = query_block(gm.seq, qb);
+    if (qbk.q0 >= gm.seq)
+        return;
+
+    stage_window<RM>(p, box, smem, tid, kThreads);
+    __syncthreads();
+    const Staged s = staged(p, smem);
+
+    const int lr = lane & 31;
+    const int g = lane >> 5;
+    const bool wave_active = qbk.q0 + wave * 32 < qbk.q1;
+    const int qrow = qbk.q0 + wave * 32 + lr;
+    const int qrow_c = min(qrow, gm.seq - 1);
+    const RopeBase rb = rope_base(box);
+
+    // query loads go first: the fetches of tiles 0 and 1 issued after them
+    // stay in flight while the query prologue waits for its own data
+    QueryRaw<TI> qraw;
+    query_load<TI>(p, s, box, head, qrow_c, g, qraw);
+    const int last_tile = gm.nkb - 1;
+    if constexpr (TI::kDma)
+    {
+        if (loader)
+        {
+            dma_tile<TI>(p, gm, s, smem, head, 0, wave, lane);
+            if (last_tile >= 1)
+                dma_tile<TI>(p, gm, s, smem, head, 1, wave, lane);
+        }
+    }
+    bf16x8 qf[8];
+    query_finish<TI, RM>(p, s, box, qrow_c, g, qraw, qf);
+
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+        o[dt] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+
+    if (loader)
+    {
+        if constexpr (TI::kDma)
+        {
+            // tile 0 has landed once at most tile 1's four fetches are outstanding
+            if (last_tile >= 1)
+                __builtin_amdgcn_s_waitcnt(kWaitVmcnt4);
+            else
+                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            prepare_tile<TI, RM>(p, gm, s, rb, smem, 0, wave, lane);
+        }
+        else
+        {
+            load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, 0, tid);
+        }
+    }
+    __syncthreads();
+
+    auto valid_keys = [&](int kb) {
+        return kb < gm.ntb ? p.text_len - kb * kBlockN : gm.vlen - (kb - gm.ntb) * kBlockN;
+    };
+    for (int kb = 0; kb < gm.nkb; kb++)
+    {
+        // attend tile kb, prepare tile kb+1 (fetched one step earlier), then
+        // fetch tile kb+2 into the buffers tile kb-1 used.  The fetch goes
+        // after the prepare: LDS reads that may alias an LDS fetch in flight
+        // wait for all of them, so a fetch issued earlier in the step would
+        // be waited for here.
+        const int ln = opaque(lane);
+        if (wave_active)
+        {
+            const char* kt = k_tile(smem, p, kb);
+            const uint16_t* vt = reinterpret_cast<const uint16_t*>(vt_tile(smem, p, kb));
+            const int nv = valid_keys(kb);
+            attend_subtile(p, kt, vt, 0, qf, nv, ln, o, m_run, l_run);
+            if (nv > 32)
+                attend_subtile(p, kt, vt, 1, qf, nv - 32, ln, o, m_run, l_run);
+        }
+        if (loader && kb + 1 < gm.nkb)
+        {
+            if constexpr (TI::kDma)
+            {
+                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // tile kb+1 has landed
+                prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+                if (kb + 2 <= last_tile)
+                    dma_tile<TI>(p, gm, s, smem, head, kb + 2, wave, ln);
+            }
+            else
+            {
+                load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, kb + 1, opaque(tid));
+            }
+        }
+        __syncthreads();
+    }
+
+    if (!wave_active)
+        return;
+    const float l_tot = partner_sum(l_run);
+    if (qrow >= qbk.q1)
+        return;
+    const float inv_l = 1.f / l_tot;
+    if (p.out_dtype == SV2_F32)
+        write_outputs<F32>(p, s, box, wi, head, qrow, g, o, inv_l);
+    else if (p.out_dtype == SV2_F16)
+        write_outputs<F16>(p, s, box, wi, head, qrow, g, o, inv_l);
+    else
+        write_outputs<BF16>(p, s, box, wi, head, qrow, g, o, inv_l);
 }
 
 // Text outputs: sum of the per-window bf16 partials in window order, then a
@@ -1014,11 +1244,11 @@ __global__ __launch_bounds__(256) void text_window_reduce_kernel(const uint32_t*
 // operand-layout path, keys 16 lanes per row, values as the fp16 operands;
 // text rows from the prepared workspace.  One workgroup (4 waves) per
 // (window, head, 32 rows).
-template <typename TI>
+template <typename TI, int RM>
 __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb, float* q_out, float* k_out,
                                                           float* v_out)
 {
-    __shared__ WindowLds lds;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
     const int blk = blockIdx.x;
     const int rb = blk % nrb;
     const int rest = blk / nrb;
@@ -1029,8 +1259,9 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
     if (rb * 32 >= seq)
         return;
     const int tid = threadIdx.x;
-    stage_window(p, box, lds, tid, 256);
+    stage_window<RM>(p, box, smem, tid, 256);
     __syncthreads();
+    const Staged s = staged(p, smem);
     const long long q_col = static_cast<long long>(head) * kHeadDim;
     const long long seq_base = static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len;
 
@@ -1039,8 +1270,10 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         const int lr = tid & 31;
         const int g = tid >> 5;
         const int j = rb * 32 + lr;
+        QueryRaw<TI> raw;
+        query_load<TI>(p, s, box, head, min(j, seq - 1), g, raw);
         bf16x8 qf[8];
-        query_operand<TI>(p, box, lds, head, min(j, seq - 1), g, qf);
+        query_finish<TI, RM>(p, s, box, min(j, seq - 1), g, raw, qf);
         if (j < seq)
         {
 #pragma unroll
@@ -1051,7 +1284,7 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         }
     }
     const int d0 = (tid & 15) * 8;
-    const KeyRope kr = key_rope(p, rope_base(box), d0);
+    const KeyRope kr = key_rope<RM>(rope_base(box), d0);
     for (int pass = 0; pass < 2; pass++)
     {
         const int j = rb * 32 + pass * 16 + (tid >> 4);
@@ -1060,12 +1293,12 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         const long long o = (seq_base + j) * p.dim + q_col + d0;
         if (jc < box.vlen)
         {
-            const int2 vr = lds.vrows[jc];
+            const int2 vr = s.rows[jc];
             float k[8];
             float v[8];
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + p.dim + d0, k);
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 2LL * p.dim + d0, v);
-            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk(p, lds, kr, k, d0, static_cast<uint32_t>(vr.y)));
+            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk<RM>(p, s, kr, k, d0, static_cast<uint32_t>(vr.y)));
             if (valid)
             {
 #pragma unroll
@@ -1141,8 +1374,51 @@ Workspace workspace_layout(const AttnParams& p)
     return w;
 }
 
+int align16(int v)
+{
+    return (v + 15) & ~15;
+}
+
+// LDS of the attention kernel for a plan: key/value tiles plus the staged
+// row table, RoPE rows and gammas of the largest window.
+LdsLayout lds_layout(int vmax, int rope_rows, bool dma)
+{
+    LdsLayout l;
+    int off = 0;
+    l.k = off;
+    off += 3 * kTileBytes;
+    l.vraw = off;
+    off += dma ? 2 * kTileBytes : 0;
+    l.vt = off;
+    off += 2 * kTileBytes;
+    l.rows = off;
+    off = align16(off + vmax * 8);
+    l.rope = off;
+    off = align16(off + rope_rows * kRopePairSlots * 8);
+    l.gamma = off;
+    off += 2 * kHeadDim * 4;
+    l.total = off;
+    return l;
+}
+
+// LDS of the prologue debug kernel (no tiles).
+LdsLayout lds_layout_staging(int vmax, int rope_rows)
+{
+    LdsLayout l;
+    l.k = l.vraw = l.vt = 0;
+    int off = 0;
+    l.rows = off;
+    off = align16(off + vmax * 8);
+    l.rope = off;
+    off = align16(off + rope_rows * kRopePairSlots * 8);
+    l.gamma = off;
+    off += 2 * kHeadDim * 4;
+    l.total = off;
+    return l;
+}
+
 // Validates the attention arguments and fills the kernel parameters.
-int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
+int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out, int* rope_rows_out)
 {
     if (!a)
         return set_error(SV2_EINVAL, "attention: null args");
@@ -1171,18 +1447,27 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
             return set_error(SV2_EINVAL, "attention: rope table missing or covering too few positions");
     }
     int smax = 0;
+    int vmax = 0;
+    int rope_rows = 0;
     for (int wi = 0; wi < p->plan.nwin; wi++)
     {
         const WindowBox b = window_box(p->plan, wi);
         if (b.vlen > kMaxVideoRows)
             return set_error(SV2_EUNSUPPORTED, "attention: a window holds more than 4096 video tokens");
-        if (b.lt + b.lh + b.lw > kMaxRopeRows || b.lt > 1023 || b.lh > 1023 || b.lw > 1023)
-            return set_error(SV2_EUNSUPPORTED, "attention: window extents beyond the staged RoPE rows (t+h+w <= 160)");
+        if (b.lt > 1023 || b.lh > 1023 || b.lw > 1023)
+            return set_error(SV2_EUNSUPPORTED, "attention: window extent beyond 1023 on an axis");
         smax = std::max(smax, b.vlen + a->text_len);
+        vmax = std::max(vmax, b.vlen);
+        rope_rows = std::max(rope_rows, b.lt + b.lh + b.lw);
     }
+    if (a->rope_mode == SV2_ROPE_NONE)
+        rope_rows = 0;
     const int64_t qkv_elems = static_cast<int64_t>(a->rule.frames) * a->rule.height * a->rule.width * 3 * a->heads * kHeadDim;
     if (qkv_elems >= (int64_t(1) << 40))
         return set_error(SV2_EUNSUPPORTED, "attention: qkv tensor too large");
+    p->lds = lds_layout(vmax, rope_rows, a->qkv_dtype != SV2_F32);
+    if (p->lds.total > kMaxLds)
+        return set_error(SV2_EUNSUPPORTED, "attention: the window's staged tables exceed the LDS of a CU");
     p->vid_qkv = a->vid_qkv;
     p->txt_qkv = a->txt_qkv;
     p->dim = a->heads * kHeadDim;
@@ -1193,8 +1478,8 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
     p->npairs = p->plan.nwin * a->heads;
     p->nqb = (smax + kRowsPerGroup - 1) / kRowsPerGroup;
     p->qk_norm = a->qk_norm ? 1 : 0;
-    p->rope_mode = a->rope_mode;
     p->rope_npos = a->rope_npos;
+    p->out_dtype = a->out_dtype;
     p->eps = a->eps;
     p->score_log2 = (1.f / std::sqrt(static_cast<float>(kHeadDim))) * kLog2e;
     p->gq_vid = a->gamma_q_vid;
@@ -1205,6 +1490,8 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out)
     p->vid_out = a->vid_out;
     p->dbg_pre = a->debug_pre;
     *smax_out = smax;
+    *vmax_out = vmax;
+    *rope_rows_out = rope_rows;
     return SV2_OK;
 }
 
@@ -1221,32 +1508,37 @@ int bind_workspace(const sv2_attn_args* a, AttnParams* p)
     return SV2_OK;
 }
 
-template <typename TI>
+template <typename TI, int RM>
 void launch_text_prepare(const AttnParams& p, hipStream_t stream)
 {
     const dim3 grid((p.text_pad + kPrepRows - 1) / kPrepRows, p.heads);
-    hipLaunchKernelGGL(text_prepare_kernel<TI>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((text_prepare_kernel<TI, RM>), grid, dim3(256), 0, stream, p);
 }
 
-template <typename TI, typename TO>
-void launch_attention(const AttnParams& p, hipStream_t stream)
+template <typename TI, int RM>
+int launch_attention(const AttnParams& p, hipStream_t stream)
 {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&window_attention_kernel<TI, RM>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, p.lds.total);
+    if (err != hipSuccess)
+        return hip_error(err, "window attention: dynamic LDS attribute");
+    if (p.text_len > 0)
+        launch_text_prepare<TI, RM>(p, stream);
     const int groups = (p.npairs + 7) / 8;
     const unsigned grid = static_cast<unsigned>(groups) * 8u * static_cast<unsigned>(p.nqb);
-    hipLaunchKernelGGL((window_attention_kernel<TI, TO>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((window_attention_kernel<TI, RM>), dim3(grid), dim3(kThreads), p.lds.total, stream, p);
+    err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "window attention launch");
 }
 
 template <typename TI>
-void launch_all(const AttnParams& p, int out_dtype, hipStream_t stream)
+int launch_rope(const AttnParams& p, int rope_mode, hipStream_t stream)
 {
-    if (p.text_len > 0)
-        launch_text_prepare<TI>(p, stream);
-    if (out_dtype == SV2_F32)
-        launch_attention<TI, F32>(p, stream);
-    else if (out_dtype == SV2_F16)
-        launch_attention<TI, F16>(p, stream);
-    else
-        launch_attention<TI, BF16>(p, stream);
+    if (rope_mode == SV2_ROPE_REFERENCE)
+        return launch_attention<TI, SV2_ROPE_REFERENCE>(p, stream);
+    if (rope_mode == SV2_ROPE_ABSOLUTE)
+        return launch_attention<TI, SV2_ROPE_ABSOLUTE>(p, stream);
+    return launch_attention<TI, SV2_ROPE_NONE>(p, stream);
 }
 
 template <typename TO>
@@ -1259,6 +1551,29 @@ void launch_reduce(const AttnParams& p, void* out, hipStream_t stream)
                        reinterpret_cast<const uint32_t*>(p.partial), out, p.plan.nwin, pairs, inv_nw);
 }
 
+template <typename TI, int RM>
+int launch_prologue(const AttnParams& p, int nrb, float* q_out, float* k_out, float* v_out, hipStream_t stream)
+{
+    if (p.text_len > 0)
+        launch_text_prepare<TI, RM>(p, stream);
+    const unsigned grid = static_cast<unsigned>(p.plan.nwin) * p.heads * nrb;
+    hipLaunchKernelGGL((qk_prologue_kernel<TI, RM>), dim3(grid), dim3(256), p.lds.total, stream, p, nrb, q_out,
+                       k_out, v_out);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "qk_prologue launch");
+}
+
+template <typename TI>
+int launch_prologue_rope(const AttnParams& p, int rope_mode, int nrb, float* q_out, float* k_out, float* v_out,
+                         hipStream_t stream)
+{
+    if (rope_mode == SV2_ROPE_REFERENCE)
+        return launch_prologue<TI, SV2_ROPE_REFERENCE>(p, nrb, q_out, k_out, v_out, stream);
+    if (rope_mode == SV2_ROPE_ABSOLUTE)
+        return launch_prologue<TI, SV2_ROPE_ABSOLUTE>(p, nrb, q_out, k_out, v_out, stream);
+    return launch_prologue<TI, SV2_ROPE_NONE>(p, nrb, q_out, k_out, v_out, stream);
+}
+
 } // namespace
 } // namespace sv2
 
@@ -1268,8 +1583,8 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args)
 {
     using namespace sv2;
     AttnParams p;
-    int smax = 0;
-    const int rc = prepare(args, &p, &smax);
+    int smax = 0, vmax = 0, rope_rows = 0;
+    const int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
     if (rc != SV2_OK)
         return rc;
     return workspace_layout(p).total;
@@ -1279,8 +1594,8 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
 {
     using namespace sv2;
     AttnParams p;
-    int smax = 0;
-    int rc = prepare(args, &p, &smax);
+    int smax = 0, vmax = 0, rope_rows = 0;
+    int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
     if (rc != SV2_OK)
         return rc;
     if (!args->vid_out || (args->text_len > 0 && !args->txt_out))
@@ -1290,14 +1605,13 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
 
     if (args->qkv_dtype == SV2_F32)
-        launch_all<F32>(p, args->out_dtype, stream);
+        rc = launch_rope<F32>(p, args->rope_mode, stream);
     else if (args->qkv_dtype == SV2_F16)
-        launch_all<F16>(p, args->out_dtype, stream);
+        rc = launch_rope<F16>(p, args->rope_mode, stream);
     else
-        launch_all<BF16>(p, args->out_dtype, stream);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess)
-        return hip_error(err, "window attention launch");
+        rc = launch_rope<BF16>(p, args->rope_mode, stream);
+    if (rc != SV2_OK)
+        return rc;
 
     if (p.text_len > 0)
     {
@@ -1307,7 +1621,7 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
             launch_reduce<F16>(p, args->txt_out, stream);
         else
             launch_reduce<BF16>(p, args->txt_out, stream);
-        err = hipGetLastError();
+        const hipError_t err = hipGetLastError();
         if (err != hipSuccess)
             return hip_error(err, "text_window_reduce_kernel launch");
     }
@@ -1318,39 +1632,22 @@ int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float
 {
     using namespace sv2;
     AttnParams p;
-    int smax = 0;
-    int rc = prepare(args, &p, &smax);
+    int smax = 0, vmax = 0, rope_rows = 0;
+    int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
     if (rc != SV2_OK)
         return rc;
     if (!q_out || !k_out || !v_out)
         return set_error(SV2_EINVAL, "qk_prologue: null output pointer");
     if ((rc = bind_workspace(args, &p)) != SV2_OK)
         return rc;
+    p.lds = lds_layout_staging(vmax, rope_rows);
     const int nrb = (smax + 31) / 32;
-    const unsigned grid = static_cast<unsigned>(p.plan.nwin) * p.heads * nrb;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (args->qkv_dtype == SV2_F32)
-    {
-        if (p.text_len > 0)
-            launch_text_prepare<F32>(p, stream);
-        hipLaunchKernelGGL(qk_prologue_kernel<F32>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
-    }
-    else if (args->qkv_dtype == SV2_F16)
-    {
-        if (p.text_len > 0)
-            launch_text_prepare<F16>(p, stream);
-        hipLaunchKernelGGL(qk_prologue_kernel<F16>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
-    }
-    else
-    {
-        if (p.text_len > 0)
-            launch_text_prepare<BF16>(p, stream);
-        hipLaunchKernelGGL(qk_prologue_kernel<BF16>, dim3(grid), dim3(256), 0, stream, p, nrb, q_out, k_out, v_out);
-    }
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess)
-        return hip_error(err, "qk_prologue launch");
-    return SV2_OK;
+        return launch_prologue_rope<F32>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
+    if (args->qkv_dtype == SV2_F16)
+        return launch_prologue_rope<F16>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
+    return launch_prologue_rope<BF16>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
 }
 
 int sv2_window_index_map(const sv2_window_rule* rule, int32_t* out, void* stream_ptr)
