@@ -14,21 +14,22 @@
 //                         evenly over several workgroups).  Every video row of
 //                         the window is located through a per-window row table
 //                         built in LDS from the closed-form plan (no
-//                         materialised window copies).  Key/value tiles of 64
-//                         keys are fetched by waves 0-7 straight from global
-//                         memory into LDS (global_load_lds, no staging
-//                         registers), two tiles ahead; the same waves then run
-//                         the k prologue (RMSNorm * gamma, RoPE, bf16) in
-//                         place on the tile and write v, rounded to bf16 and
-//                         held as fp16, transposed.  Each wave owns 32 query
-//                         rows whose q prologue runs in registers.
-//                         S^T = K Q^T on bf16 MFMA (exact operands), online
-//                         softmax per 32-key subtile in fp32 with lazy
-//                         rescaling, O^T += V^T P^T on fp16 MFMA.  Ragged
-//                         windows: keys past the window are masked, query rows
-//                         past it are not stored.  Video outputs are written
-//                         once (the windows partition the grid), text outputs
-//                         to per-window bf16 partials;
+//                         materialised window copies).  Key and value tiles of
+//                         64 keys move from global memory straight into LDS
+//                         (global_load_lds, no staging registers), two tiles
+//                         ahead: waves 0-7 fetch the key tile and run the k
+//                         prologue (RMSNorm * gamma, RoPE, bf16) in place,
+//                         waves 8-11 fetch the value tile and write v, rounded
+//                         to bf16 and held as fp16, transposed.  Each wave
+//                         owns 32 query rows whose q prologue runs in
+//                         registers.  S^T = K Q^T on bf16 MFMA (exact
+//                         operands), online softmax per 32-key subtile in fp32
+//                         with lazy rescaling (row max / sum exchanged between
+//                         half-waves with v_permlane32_swap), O^T += V^T P^T on
+//                         fp16 MFMA.  Ragged windows: keys past the window are
+//                         masked, query rows past it are not stored.  Video
+//                         outputs are written once (the windows partition the
+//                         grid), text outputs to per-window bf16 partials;
 //   text_window_reduce_kernel
 //                         text outputs: partials summed in window order, times
 //                         1/nW, as the reference accumulates them.
@@ -52,7 +53,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kWaves = 12;
 constexpr int kThreads = kWaves * 64;        // 768
-constexpr int kLoaderThreads = 512;          // waves 0-7 fetch and prepare key/value tiles
+constexpr int kLoaderThreads = 512;          // fp32 inputs: waves 0-7 load and prepare key/value tiles
 constexpr int kRowsPerGroup = kWaves * 32;   // query rows per workgroup
 constexpr int kBlockN = 64;                  // keys per tile
 constexpr int kTileBytes = kBlockN * kHeadDim * 2; // one K, V or V^T tile of 16-bit values
@@ -63,8 +64,9 @@ constexpr int kPrepRows = 16;                // text rows per text_prepare workg
 constexpr int kMaxLds = 160 * 1024;          // LDS of one gfx950 CU
 // s_waitcnt immediates for vmcnt(0) / vmcnt(4) with expcnt and lgkmcnt left
 // unconstrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
-// vmcnt[5:4] << 14).  Each loader lane issues exactly four fetches per tile.
+// vmcnt[5:4] << 14).
 constexpr int kWaitVmcnt0 = 0x0F70;
+constexpr int kWaitVmcnt2 = 0x0F72;
 constexpr int kWaitVmcnt4 = 0x0F74;
 constexpr float kRescaleLog2 = 8.f;          // O is rescaled only when a row max grows by more than 2^8
 constexpr float kLog2e = 1.4426950408889634f;
@@ -273,14 +275,21 @@ __device__ inline float row16_sum(float v)
     return v;
 }
 
-// The value of lane l and of lane l^32 (ds_bpermute).  Both lanes of a pair
-// then reduce the same two operands, so they agree bit for bit.
+// The values of lanes l % 32 and l % 32 + 32 (v_permlane32_swap, a VALU op
+// exchanging the upper half-wave of one register with the lower half-wave of
+// another): starting from two copies of v, one register ends up holding the
+// lower half-wave's values in every lane and the other the upper half-wave's,
+// so both lanes of a pair receive the two operands in the same order and the
+// reductions below agree bit for bit.  Written as inline assembly (with the
+// wait states a VALU write needs before a permlane read): the compiler's
+// builtin for this instruction treats its two results as one value.
 __device__ inline void with_partner(float v, float* a, float* b)
 {
-    const float w = __shfl_xor(v, 32);
-    const bool low = (threadIdx.x & 32) == 0;
-    *a = low ? v : w;
-    *b = low ? w : v;
+    float x = v;
+    float y = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+    *a = x;
+    *b = y;
 }
 
 __device__ inline float partner_max(float v)
@@ -381,12 +390,21 @@ __device__ inline int key_perm(int i)
     return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
-// Byte offset of chunk c (dims 8c..8c+7) of row r in a key tile: 16-byte
-// slots, XOR-swizzled so the MFMA operand reads of 16 rows hit 16 different
-// slot positions.
+// Byte offset of chunk c (dims 8c..8c+7) of row r in a key tile.  The tile is
+// split into two 8 KB halves (dims 0-63, 64-127); in a half, row r holds 8
+// 16-byte slots at r * 128 and chunk c & 7 sits in slot (c & 7) ^ ((r >> 1) & 7).
+// The MFMA operand reads of 16 consecutive rows then hit 16 different slot
+// positions, and a lane's eight reads of one row are four per-lane bases plus
+// immediate offsets (half * 8192).
 __device__ inline int k_slot_offset(int r, int c)
 {
-    return (r * 16 + (c ^ (r & 15))) * 16;
+    return (c >> 3) * 8192 + r * 128 + (((c & 7) ^ ((r >> 1) & 7)) << 4);
+}
+
+// Byte offset of chunk c of row r in a raw value tile (same halves, no swizzle).
+__device__ inline int vraw_offset(int r, int c)
+{
+    return (c >> 3) * 8192 + r * 128 + ((c & 7) << 4);
 }
 
 // Swizzled offset (in halfs) of key group `grp` (8 keys, 0..7) in row d of the
@@ -420,9 +438,20 @@ __device__ inline int opaque(int v)
     return v;
 }
 
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i
+// writes LDS bytes [lds + 16 i, lds + 16 i + 16), lds being wave-uniform.
+// Issued through inline assembly so that the compiler does not treat later
+// LDS reads as possibly depending on it (it would otherwise wait for every
+// fetch in flight before any LDS read); the kernel places the vmcnt waits
+// itself.  M0 (the LDS base of the copy) is saved and restored.
 __device__ inline void dma16(const void* g, char* lds)
 {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+    const unsigned base = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<size_t>(lds)));
+    unsigned saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(base), "v"(g)
+                 : "memory");
 }
 
 // ---------------------------------------------------------------- per-window staging
@@ -747,66 +776,78 @@ __device__ inline char* vt_tile(char* smem, const AttnParams& p, int kb)
     return smem + p.lds.vt + (kb & 1) * kTileBytes;
 }
 
-// 16-bit inputs: waves 0-7 move tile kb from global memory straight into LDS,
-// four 1 KB wave-instructions per wave (the lane order fixes where each
-// 16-byte chunk lands).  Wave w fetches key rows 4w..4w+3 and 32+4w..32+4w+3
-// of the key tile (swizzled) and value rows 8w..8w+7 — exactly the rows it
-// prepares afterwards, so no barrier separates the fetch from the prologue.
-// Rows past the end of a ragged tile repeat the last valid row: their scores
-// are masked and their values multiply p = 0.
+// 16-bit inputs: tile kb moves from global memory straight into LDS, one 1 KB
+// wave-instruction at a time (the lane order fixes where each 16-byte chunk
+// lands).  Waves 0-7 fetch the key tile, wave w rows 8w..8w+7, one half (64
+// dims) per instruction, lane l taking row 8w + l / 8; waves 8-11 fetch the
+// value tile, wave 8+v rows 16v..16v+15 in four instructions.  Each wave
+// prepares exactly the rows it fetched, so no barrier separates the fetch
+// from the prologue.  Rows past the end of a ragged tile repeat the last
+// valid row: their scores are masked and their values multiply p = 0.
+// Fetches per lane and tile: 2 (key waves), 4 (value waves).
 template <typename TI>
 __device__ inline void dma_tile(const AttnParams& p, const Geometry& gm, const Staged& s, char* smem, int head,
                                 int kb, int wave, int lane)
 {
-    char* kt = k_tile(smem, p, kb);
+    const int sl = lane & 7;
+    if (wave < 8)
+    {
+        char* kt = k_tile(smem, p, kb);
+        const int r = 8 * wave + (lane >> 3);
+        const int ksl = sl ^ ((r >> 1) & 7); // chunk (within the half) the swizzled slot holds
+        const uint16_t* krow;
+        if (kb < gm.ntb)
+            krow = p.txt_k + (static_cast<long long>(head) * p.text_len + min(kb * kBlockN + r, p.text_len - 1)) *
+                                 kHeadDim;
+        else
+            krow = static_cast<const uint16_t*>(p.vid_qkv) +
+                   static_cast<long long>(s.rows[min((kb - gm.ntb) * kBlockN + r, gm.vlen - 1)].x) * p.row_stride +
+                   p.dim + head * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            dma16(krow + 8 * (8 * i + ksl), kt + i * 8192 + 8 * wave * 128);
+        return;
+    }
     char* vr = vraw_tile(smem, p, kb);
-    const int sub = lane >> 4;
-    const int slot = lane & 15;
+    const int v = wave - 8;
     if (kb < gm.ntb)
     {
-        const int base = kb * kBlockN;
-        const long long kbase = static_cast<long long>(head) * p.text_len;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-        {
-            const int r = 32 * i + 4 * wave + sub;
-            const int l = min(base + r, p.text_len - 1);
-            const int c = slot ^ (r & 15);
-            dma16(p.txt_k + (kbase + l) * kHeadDim + 8 * c, kt + (32 * i + 4 * wave) * 256);
-        }
         // V^T slots: instruction q covers rows d = 8q .. 8q+7 of the transposed tile
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < 4; i++)
         {
-            const int q = 2 * wave + i;
+            const int q = 4 * v + i;
             const int d = 8 * q + (lane >> 3);
-            const int sl = lane & 7;
             const int grp = sl ^ ((d ^ (d >> 3)) & 7);
-            dma16(p.txt_vt + (static_cast<long long>(head) * kHeadDim + d) * p.text_pad + base + 8 * grp,
+            dma16(p.txt_vt + (static_cast<long long>(head) * kHeadDim + d) * p.text_pad + kb * kBlockN + 8 * grp,
                   vr + q * 1024);
         }
         return;
     }
-    const int base = (kb - gm.ntb) * kBlockN;
-    const int last = gm.vlen - 1;
-    const long long k_col = static_cast<long long>(p.dim) + static_cast<long long>(head) * kHeadDim;
-    const long long v_col = k_col + p.dim;
-    const uint16_t* src = static_cast<const uint16_t*>(p.vid_qkv);
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int b = 0; b < 2; b++)
     {
-        const int r = 32 * i + 4 * wave + sub;
-        const int c = slot ^ (r & 15);
-        const int row = s.rows[min(base + r, last)].x;
-        dma16(src + static_cast<long long>(row) * p.row_stride + k_col + 8 * c, kt + (32 * i + 4 * wave) * 256);
-    }
+        const int r = 16 * v + 8 * b + (lane >> 3);
+        const uint16_t* vrow = static_cast<const uint16_t*>(p.vid_qkv) +
+                               static_cast<long long>(s.rows[min((kb - gm.ntb) * kBlockN + r, gm.vlen - 1)].x) *
+                                   p.row_stride +
+                               2LL * p.dim + head * kHeadDim;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-    {
-        const int r = 8 * wave + 4 * i + sub;
-        const int row = s.rows[min(base + r, last)].x;
-        dma16(src + static_cast<long long>(row) * p.row_stride + v_col + 8 * slot, vr + (8 * wave + 4 * i) * 256);
+        for (int h = 0; h < 2; h++)
+            dma16(vrow + 8 * (8 * h + sl), vr + h * 8192 + (16 * v + 8 * b) * 128);
     }
+}
+
+// Waits until this lane's fetches of the older of the (at most) two tiles in
+// flight have landed: key waves issue 2 fetches per tile, value waves 4.
+__device__ inline void wait_tile_fetch(int wave, bool newer_in_flight)
+{
+    if (!newer_in_flight)
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    else if (wave < 8)
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt2);
+    else
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt4);
 }
 
 // Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0).
@@ -819,47 +860,57 @@ __device__ inline void store_vt_pair(char* vt, int r, int d0, const float v0[8],
         *reinterpret_cast<f16x2*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = bf16_pair_as_f16(v0[e], v1[e]);
 }
 
-// 16-bit inputs: the prologue of tile kb, run by the wave that fetched it
-// (after its own fetch has landed).  Video: k in place (RMSNorm * gamma, RoPE,
-// bf16), v rounded to bf16 and transposed into the V^T tile.  Text (prepared
-// in the workspace): the V^T slots are copied to the V^T tile.
+// 16-bit inputs: the prologue of tile kb, run by the waves that fetched it
+// (after their own fetches have landed).  Video: waves 0-7 run the k
+// prologue (RMSNorm * gamma, RoPE, bf16) in place, waves 8-11 round v to bf16
+// and write it transposed into the V^T tile.  Text (prepared in the
+// workspace): waves 8-11 copy the V^T slots to the V^T tile.
 template <typename TI, int RM>
 __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, const Staged& s, const RopeBase& rb,
                                     char* smem, int kb, int wave, int lane)
 {
-    char* vt = vt_tile(smem, p, kb);
-    const char* vr = vraw_tile(smem, p, kb);
-    if (kb < gm.ntb)
+    const int chunk = lane & 15;
+    const int d0 = chunk * 8;
+    if (wave < 8)
     {
+        if (kb < gm.ntb)
+            return;
+        char* kt = k_tile(smem, p, kb);
+        const int base = (kb - gm.ntb) * kBlockN;
+        const int last = gm.vlen - 1;
+        const KeyRope kr = key_rope<RM>(rb, d0);
 #pragma unroll
         for (int i = 0; i < 2; i++)
         {
-            const int off = (2 * wave + i) * 1024 + lane * 16;
+            const int r = 8 * wave + 4 * i + (lane >> 4);
+            uint4* slot = reinterpret_cast<uint4*>(kt + k_slot_offset(r, chunk));
+            uint4 raw[1] = {*slot};
+            float x[8];
+            raw8_to_float<TI>(raw, x);
+            const uint32_t packed = static_cast<uint32_t>(s.rows[min(base + r, last)].y);
+            *slot = key_chunk<RM>(p, s, kr, x, d0, packed);
+        }
+        return;
+    }
+    char* vt = vt_tile(smem, p, kb);
+    const char* vr = vraw_tile(smem, p, kb);
+    const int v = wave - 8;
+    if (kb < gm.ntb)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+        {
+            const int off = (4 * v + i) * 1024 + lane * 16;
             *reinterpret_cast<uint4*>(vt + off) = *reinterpret_cast<const uint4*>(vr + off);
         }
         return;
     }
-    char* kt = k_tile(smem, p, kb);
-    const int base = (kb - gm.ntb) * kBlockN;
-    const int last = gm.vlen - 1;
-    const int chunk = lane & 15;
-    const int d0 = chunk * 8;
-    const KeyRope kr = key_rope<RM>(rb, d0);
 #pragma unroll
     for (int i = 0; i < 2; i++)
     {
-        const int r = 32 * i + 4 * wave + (lane >> 4);
-        uint4* slot = reinterpret_cast<uint4*>(kt + k_slot_offset(r, chunk));
-        uint4 raw[1] = {*slot};
-        float x[8];
-        raw8_to_float<TI>(raw, x);
-        const uint32_t packed = static_cast<uint32_t>(s.rows[min(base + r, last)].y);
-        *slot = key_chunk<RM>(p, s, kr, x, d0, packed);
-    }
-    {
-        const int r = 4 * wave + (lane >> 4); // keys 2r, 2r+1 = rows 8w + 2 (lane >> 4) (+1) of the raw tile
-        uint4 a[1] = {*reinterpret_cast<const uint4*>(vr + ((2 * r) * 16 + chunk) * 16)};
-        uint4 b[1] = {*reinterpret_cast<const uint4*>(vr + ((2 * r + 1) * 16 + chunk) * 16)};
+        const int r = 8 * v + 4 * i + (lane >> 4); // keys 2r, 2r+1 (rows 16v..16v+15 of the raw tile)
+        uint4 a[1] = {*reinterpret_cast<const uint4*>(vr + vraw_offset(2 * r, chunk))};
+        uint4 b[1] = {*reinterpret_cast<const uint4*>(vr + vraw_offset(2 * r + 1, chunk))};
         float v0[8];
         float v1[8];
         raw8_to_float<TI>(a, v0);
@@ -925,16 +976,44 @@ __device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry
 
 // ---------------------------------------------------------------- attention step
 
-// One 32-key subtile of the online softmax for the wave's 32 query rows.
-__device__ inline void attend_subtile(const AttnParams& p, const char* kt, const uint16_t* vt, int kt_idx,
-                                      const bf16x8 qf[8], int nvalid, int lane, f32x16 o[4], float& m_run,
-                                      float& l_run)
+// Per-lane byte offsets of the MFMA operand reads, fixed for the whole loop:
+// kb4[j] = row key_perm(lr) of the key tile, chunk 2j + g (dims 16j + 8g),
+// half 0; chunk 2c + g is kb4[c & 3] + (c >> 2) * 8192, subtile kt adds
+// kt * 4096.  vb4[m] = row lr of the V^T tile, key group
+// (g ^ f(lr)) ^ 2m with f(d) = (d ^ (d >> 3)) & 7; the read of rows
+// dt * 32 + lr, key group 4 kt + 2 c2 + g is vb4[c2 + 2 (kt ^ (dt & 1))] +
+// dt * 4096 (the swizzle of row dt * 32 + lr is f(lr) ^ 4 (dt & 1)).
+struct ReadBases
+{
+    int k[4];
+    int v[4];
+};
+
+__device__ inline ReadBases read_bases(int lane)
 {
     const int lr = lane & 31;
     const int g = lane >> 5;
+    ReadBases b;
+    const int r = key_perm(lr);
+    const int y = (r >> 1) & 7;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        b.k[j] = r * 128 + (((2 * j + g) ^ y) << 4);
+    const int u = g ^ ((lr ^ (lr >> 3)) & 7);
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        b.v[m] = lr * 128 + ((u ^ (2 * m)) << 4);
+    return b;
+}
+
+// One 32-key subtile of the online softmax for the wave's 32 query rows.
+template <int KT>
+__device__ inline void attend_subtile(const AttnParams& p, const char* kt, const char* vt, const ReadBases& rb,
+                                      const bf16x8 qf[8], int nvalid, int g, f32x16 o[4], float& m_run,
+                                      float& l_run)
+{
     // ---- S^T = K Q^T for 32 keys; K fragments are read four at a time ahead
     // of the MFMAs that consume them
-    const int row = kt_idx * 32 + key_perm(lr);
     f32x16 s = f32x16{};
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -942,7 +1021,7 @@ __device__ inline void attend_subtile(const AttnParams& p, const char* kt, const
         bf16x8 a[4];
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            a[c] = *reinterpret_cast<const bf16x8*>(kt + k_slot_offset(row, 2 * (4 * h + c) + g));
+            a[c] = *reinterpret_cast<const bf16x8*>(kt + rb.k[c] + h * 8192 + KT * 4096);
 #pragma unroll
         for (int c = 0; c < 4; c++)
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c], qf[4 * h + c], s, 0, 0, 0);
@@ -987,11 +1066,10 @@ __device__ inline void attend_subtile(const AttnParams& p, const char* kt, const
 #pragma unroll
     for (int c2 = 0; c2 < 2; c2++)
     {
-        const int kgrp = kt_idx * 4 + c2 * 2 + g;
         f16x8 va[4];
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
-            va[dt] = *reinterpret_cast<const f16x8*>(vt + vt_offset(dt * 32 + lr, kgrp));
+            va[dt] = *reinterpret_cast<const f16x8*>(vt + rb.v[c2 + 2 * (KT ^ (dt & 1))] + dt * 4096);
         f16x8 b;
 #pragma unroll
         for (int e = 0; e < 8; e += 2)
@@ -1030,10 +1108,27 @@ __device__ inline QueryBlock query_block(int seq, int qb)
     return b;
 }
 
-template <typename TO>
+// Four outputs already rounded to bf16 (two packed pairs) in the output type.
+__device__ inline void store_rounded(int out_dtype, void* base, long long offset, uint32_t lo, uint32_t hi)
+{
+    const float v[4] = {__builtin_bit_cast(float, lo << 16), __builtin_bit_cast(float, lo & 0xffff0000u),
+                        __builtin_bit_cast(float, hi << 16), __builtin_bit_cast(float, hi & 0xffff0000u)};
+    if (out_dtype == SV2_BF16)
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + offset) = make_uint2(lo, hi);
+    else if (out_dtype == SV2_F16)
+        store4<F16>(base, offset, v);
+    else
+        store4<F32>(base, offset, v);
+}
+
+// Epilogue of one wave: O / l, rounded to bf16 where the reference rounds each
+// output element (seedvr2_dit_block.cpp:1074; v_cvt_pk_bf16_f32 rounds to
+// nearest even), video rows scattered to their grid rows, text rows to this
+// window's bf16 partials.
 __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const WindowBox& box, int wi, int head,
                                      int qrow, int g, const f32x16 o[4], float inv_l)
 {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
     const long long q_col = static_cast<long long>(head) * kHeadDim;
     const bool text = qrow >= box.vlen;
     long long out_off;
@@ -1043,6 +1138,8 @@ __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const
         out_off = (static_cast<long long>(wi) * p.text_len + (qrow - box.vlen)) * p.dim + q_col;
     const long long pre_row =
         (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + qrow) * p.dim + q_col;
+    void* dst = text ? static_cast<void*>(p.partial) : p.vid_out;
+    const int dt_out = text ? SV2_BF16 : p.out_dtype;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -1050,19 +1147,18 @@ __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const
         {
             const int d = dt * 32 + 8 * rq + 4 * g;
             float pre[4];
-            float rounded[4];
 #pragma unroll
             for (int e = 0; e < 4; e++)
-            {
                 pre[e] = o[dt][4 * rq + e] * inv_l;
-                rounded[e] = bf16_round(pre[e]);
-            }
+            bf16x2 a;
+            bf16x2 b;
+            a[0] = static_cast<__bf16>(pre[0]);
+            a[1] = static_cast<__bf16>(pre[1]);
+            b[0] = static_cast<__bf16>(pre[2]);
+            b[1] = static_cast<__bf16>(pre[3]);
             if (p.dbg_pre)
                 store4<F32>(p.dbg_pre, pre_row + d, pre);
-            if (!text)
-                store4<TO>(p.vid_out, out_off + d, rounded);
-            else
-                store4<BF16>(p.partial, out_off + d, rounded);
+            store_rounded(dt_out, dst, out_off + d, __builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
         }
 }
 
@@ -1109,21 +1205,18 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     const int qrow = qbk.q0 + wave * 32 + lr;
     const int qrow_c = min(qrow, gm.seq - 1);
     const RopeBase rb = rope_base(box);
+    const ReadBases rdb = read_bases(lane);
 
-    // query loads go first: the fetches of tiles 0 and 1 issued after them
-    // stay in flight while the query prologue waits for its own data
-    QueryRaw<TI> qraw;
-    query_load<TI>(p, s, box, head, qrow_c, g, qraw);
+    // the fetches of tiles 0 and 1 and the query loads are in flight together
     const int last_tile = gm.nkb - 1;
     if constexpr (TI::kDma)
     {
-        if (loader)
-        {
-            dma_tile<TI>(p, gm, s, smem, head, 0, wave, lane);
-            if (last_tile >= 1)
-                dma_tile<TI>(p, gm, s, smem, head, 1, wave, lane);
-        }
+        dma_tile<TI>(p, gm, s, smem, head, 0, wave, lane);
+        if (last_tile >= 1)
+            dma_tile<TI>(p, gm, s, smem, head, 1, wave, lane);
     }
+    QueryRaw<TI> qraw;
+    query_load<TI>(p, s, box, head, qrow_c, g, qraw);
     bf16x8 qf[8];
     query_finish<TI, RM>(p, s, box, qrow_c, g, qraw, qf);
 
@@ -1134,21 +1227,15 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    if (loader)
+    if constexpr (TI::kDma)
     {
-        if constexpr (TI::kDma)
-        {
-            // tile 0 has landed once at most tile 1's four fetches are outstanding
-            if (last_tile >= 1)
-                __builtin_amdgcn_s_waitcnt(kWaitVmcnt4);
-            else
-                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-            prepare_tile<TI, RM>(p, gm, s, rb, smem, 0, wave, lane);
-        }
-        else
-        {
-            load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, 0, tid);
-        }
+        // tile 0 has landed once at most tile 1's fetches are outstanding
+        wait_tile_fetch(wave, last_tile >= 1);
+        prepare_tile<TI, RM>(p, gm, s, rb, smem, 0, wave, lane);
+    }
+    else if (loader)
+    {
+        load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, 0, tid);
     }
     __syncthreads();
 
@@ -1157,31 +1244,35 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     };
     for (int kb = 0; kb < gm.nkb; kb++)
     {
-        // attend tile kb, prepare tile kb+1 (fetched one step earlier), then
-        // fetch tile kb+2 into the buffers tile kb-1 used.  The fetch goes
-        // after the prepare: LDS reads that may alias an LDS fetch in flight
-        // wait for all of them, so a fetch issued earlier in the step would
-        // be waited for here.
+        // fetch tile kb+2 into the buffers tile kb-1 used (all reads of them
+        // ended before the last barrier), attend tile kb, prepare tile kb+1
+        // (fetched one step earlier)
         const int ln = opaque(lane);
+        const bool fetch = kb + 2 <= last_tile;
+        if constexpr (TI::kDma)
+        {
+            if (fetch)
+                dma_tile<TI>(p, gm, s, smem, head, kb + 2, wave, ln);
+        }
         if (wave_active)
         {
             const char* kt = k_tile(smem, p, kb);
-            const uint16_t* vt = reinterpret_cast<const uint16_t*>(vt_tile(smem, p, kb));
+            const char* vt = vt_tile(smem, p, kb);
             const int nv = valid_keys(kb);
-            attend_subtile(p, kt, vt, 0, qf, nv, ln, o, m_run, l_run);
+            attend_subtile<0>(p, kt, vt, rdb, qf, nv, g, o, m_run, l_run);
             if (nv > 32)
-                attend_subtile(p, kt, vt, 1, qf, nv - 32, ln, o, m_run, l_run);
+                attend_subtile<1>(p, kt, vt, rdb, qf, nv - 32, g, o, m_run, l_run);
         }
-        if (loader && kb + 1 < gm.nkb)
+        if (kb + 1 < gm.nkb)
         {
             if constexpr (TI::kDma)
             {
-                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // tile kb+1 has landed
+                // tile kb+1 has landed once only tile kb+2's fetches (if any)
+                // are outstanding
+                wait_tile_fetch(wave, fetch);
                 prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
-                if (kb + 2 <= last_tile)
-                    dma_tile<TI>(p, gm, s, smem, head, kb + 2, wave, ln);
             }
-            else
+            else if (loader)
             {
                 load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, kb + 1, opaque(tid));
             }
@@ -1194,13 +1285,7 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     const float l_tot = partner_sum(l_run);
     if (qrow >= qbk.q1)
         return;
-    const float inv_l = 1.f / l_tot;
-    if (p.out_dtype == SV2_F32)
-        write_outputs<F32>(p, s, box, wi, head, qrow, g, o, inv_l);
-    else if (p.out_dtype == SV2_F16)
-        write_outputs<F16>(p, s, box, wi, head, qrow, g, o, inv_l);
-    else
-        write_outputs<BF16>(p, s, box, wi, head, qrow, g, o, inv_l);
+    write_outputs(p, s, box, wi, head, qrow, g, o, 1.f / l_tot);
 }
 
 // Text outputs: sum of the per-window bf16 partials in window order, then a
