@@ -180,6 +180,116 @@ int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int 
  * (:514-533). */
 int sv2_swiglu(void* gate, const void* value, int io_dtype, int64_t count, void* stream);
 
+/* ------------------------------------------------------------------------
+ * The SeedVR2DiTBlock layer (seedvr2_dit_block.h:38-172): one MM-DiT block
+ * of SeedVR2-3B on the device.  Same parameters (ids 0-8 of the layer's
+ * ParamDict, seedvr2_dit_block.cpp:643-655), the same weight order
+ * (load_branch / load_model, :657-688) and the same blob layouts (bottoms
+ * vid [L_v, dim], txt [L_txt, dim], emb [6*dim], the patched (T, H, W);
+ * tops vid_out, txt_out).  Optional ids 9-13 select variants the reference
+ * does not have (fixed window extents, absolute 3-D RoPE, no q/k norm); their
+ * defaults are the reference semantics.
+ * ------------------------------------------------------------------------ */
+
+typedef struct sv2_block_config {
+    int block_index;     /* param 0 */
+    int shared_weights;  /* param 1: one weight branch for video and text (blocks >= 10) */
+    int last_layer;      /* param 2: text skips ada input / gate, txt_out = 2 * txt_proj */
+    int shifted_window;  /* param 3 */
+    int dim;             /* param 4 (2560) */
+    int heads;           /* param 5 (20) */
+    int head_dim;        /* param 6 (128) */
+    int mlp_hidden;      /* param 7 (6912) */
+    float norm_eps;      /* param 8 (1e-5) */
+    int window_t;        /* param 9: window extent on t, 0 = the reference's adaptive rule */
+    int window_h;        /* param 10 */
+    int window_w;        /* param 11 */
+    int rope_mode;       /* param 12: sv2_rope_mode (default SV2_ROPE_REFERENCE) */
+    int qk_norm;         /* param 13: 1 (default) = per-head RMSNorm * gamma on q, k */
+} sv2_block_config;
+
+/* Weights of one branch ("vid", "txt" or the shared "all"), in the order the
+ * exporter writes them (tools/export_seedvr2_dit_ncnn.py:222-235).  Matrices
+ * are [out][in] row-major (InnerProduct layout). */
+typedef struct sv2_block_branch {
+    const void* ada[6];  /* [dim] each: attn shift, scale, gate, mlp shift, scale, gate (fp32) */
+    const void* w_qkv;   /* [3*dim][dim] */
+    const void* w_proj;  /* [dim][dim] */
+    const void* b_proj;  /* [dim] fp32 */
+    const void* norm_q;  /* [head_dim] fp32 */
+    const void* norm_k;  /* [head_dim] fp32 */
+    const void* w_gate;  /* [mlp_hidden][dim] */
+    const void* w_in;    /* [mlp_hidden][dim] */
+    const void* w_out;   /* [dim][mlp_hidden] */
+} sv2_block_branch;
+
+typedef struct sv2_block sv2_block;
+
+/* Host.  Fills `config` with the reference defaults (the exporter's block 0). */
+void sv2_block_config_default(sv2_block_config* config);
+
+/* Loads one exported block: the SeedVR2DiTBlock layer of `param_path` and
+ * its weights from `bin_path` (replaces ncnn's Net::load_param / load_model
+ * driving SeedVR2DiTBlock::load_param / load_model, seedvr2_dit_block.cpp:
+ * 643-688), then uploads the weights: matrices in `compute_dtype` (SV2_F32 or
+ * SV2_F16), vectors in fp32.  Returns SV2_OK, SV2_EINVAL (-1) for a file that
+ * does not parse or whose layer parameters are invalid (dim != heads *
+ * head_dim, as load_param), SV2_EDEVICE (-100) for a weight stream that ends
+ * early or an allocation failure (load_model's code). */
+int sv2_block_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_block** out);
+
+/* Creates a block from weights already in memory.  weights_on_device == 0:
+ * host fp32 arrays, converted and uploaded (owned by the block).
+ * weights_on_device == 1: device arrays, matrices in compute_dtype and
+ * vectors in fp32, borrowed (they must outlive the block).  `txt` is ignored
+ * when config->shared_weights.  rope_freqs: host, 21 fp32 (the block's
+ * rope.freqs), may be NULL unless rope_mode is SV2_ROPE_REFERENCE. */
+int sv2_block_create(const sv2_block_config* config, const sv2_block_branch* vid, const sv2_block_branch* txt,
+                     const float* rope_freqs, int weights_on_device, int compute_dtype, sv2_block** out);
+
+/* Host.  The parameters the block was created with. */
+int sv2_block_get_config(const sv2_block* block, sv2_block_config* config);
+
+/* The patched grid (T, H, W) of the next forward
+ * (SeedVR2DiTBlock::set_runtime_shape, seedvr2_dit_block.cpp:609-615). */
+int sv2_block_set_runtime_shape(sv2_block* block, int frames, int height, int width);
+
+/* Bytes of device workspace a forward of text_len text tokens needs at the
+ * current runtime shape. */
+int64_t sv2_block_workspace_size(const sv2_block* block, int text_len);
+
+/* Device.  One block forward (SeedVR2DiTBlock::forward, seedvr2_dit_block.cpp:
+ * 1114-1267): vid [T*H*W, dim] and txt [text_len, dim] in the compute dtype,
+ * emb [6*dim] fp32; writes vid_out, txt_out (same shapes, compute dtype).
+ * Enqueues on `stream` only.  workspace may be NULL (the block then keeps
+ * its own, grown on demand).  Returns SV2_EINVAL when the runtime shape was
+ * not set (as the layer's device forward, :1320-1321). */
+int sv2_block_forward(sv2_block* block, const void* vid, const void* txt, int text_len, const float* emb,
+                      void* vid_out, void* txt_out, void* workspace, size_t workspace_bytes, void* stream);
+
+void sv2_block_destroy(sv2_block* block);
+
+/* Intermediate captures of one forward, fp32 device arrays (any may be NULL).
+ * Replaces SeedVR2DiTBlockDebugTensors (seedvr2_dit_block.h:20-36) for the
+ * fields the block itself produces: qkv, the attention outputs (bf16-rounded,
+ * text averaged over windows; the inputs of proj_out), the projections
+ * before the gate (:1188-1192) and the outputs. */
+typedef struct sv2_block_debug {
+    float* qkv_vid;       /* [L_v, 3*dim] */
+    float* qkv_txt;       /* [L_txt, 3*dim] */
+    float* attention_vid; /* [L_v, dim] */
+    float* attention_txt; /* [L_txt, dim] */
+    float* projected_vid; /* [L_v, dim] */
+    float* projected_txt; /* [L_txt, dim] */
+    float* output_vid;    /* [L_v, dim] */
+    float* output_txt;    /* [L_txt, dim] */
+} sv2_block_debug;
+
+/* Enables captures for the following forwards (NULL disables them), as
+ * SeedVR2DiTBlock::set_debug_tensors (seedvr2_dit_block.cpp:617-620).  The
+ * struct is copied; the arrays must stay valid while captures are enabled. */
+int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug);
+
 /* Message of the last failure on the calling thread (never NULL). */
 const char* sv2_last_error(void);
 

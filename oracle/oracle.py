@@ -90,6 +90,12 @@ def load() -> ctypes.CDLL:
     lib.orc_inner_product.argtypes = [vp, i, i, vp, vp, i, vp, i]
     lib.orc_block_forward.argtypes = [ctypes.POINTER(OrcBlock), vp, i, vp, i, vp, i, i, i, vp, vp]
     lib.orc_block_forward.restype = i
+    lib.orc_block_head.argtypes = [ctypes.POINTER(OrcBlock), vp, i, vp, i, vp, vp, vp]
+    lib.orc_block_head.restype = i
+    lib.orc_block_attention.argtypes = [ctypes.POINTER(OrcBlock), i, i, i, i, vp, vp, vp, vp]
+    lib.orc_block_attention.restype = i
+    lib.orc_block_tail.argtypes = [ctypes.POINTER(OrcBlock), vp, i, vp, i, vp, vp, vp, vp, vp, vp, vp]
+    lib.orc_block_tail.restype = i
     _lib = lib
     return lib
 
@@ -206,27 +212,77 @@ BRANCH_FIELDS = ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scal
                  "w_qkv", "w_proj", "b_proj", "norm_q", "norm_k", "w_gate", "w_in", "w_out")
 
 
+class Block:
+    """One block's parameters and weights for the oracle's block functions.
+    weights: {"vid": {field: array}, "txt": {...} (unless shared), "freqs": [21]}."""
+
+    def __init__(self, weights, *, dim, heads, head_dim=128, mlp_hidden, eps=1e-5, shared=False,
+                 last_layer=False, shifted=False, wt=0, wh=0, ww=0, rope_mode=ROPE_REFERENCE, theta=10000.0,
+                 qk_norm=True, threads=0):
+        self._keep = []
+
+        def branch(d):
+            arrs = {k: _f32(d[k]) for k in BRANCH_FIELDS}
+            self._keep.append(arrs)
+            return OrcBranch(*[_p(arrs[k]) for k in BRANCH_FIELDS])
+
+        vb = branch(weights["vid"])
+        tb = vb if shared else branch(weights["txt"])
+        freqs = _f32(weights["freqs"])
+        self._keep.append(freqs)
+        self.dim = dim
+        self.s = OrcBlock(dim, heads, head_dim, mlp_hidden, eps, int(shared), int(last_layer), int(shifted),
+                          wt, wh, ww, rope_mode, theta, int(qk_norm), vb, tb, _p(freqs), threads)
+
+    def forward(self, vid, txt, emb, T, H, W):
+        vid, txt, emb = _f32(vid), _f32(txt), _f32(emb)
+        vid_out = np.zeros_like(vid)
+        txt_out = np.zeros_like(txt)
+        rc = load().orc_block_forward(ctypes.byref(self.s), _p(vid), vid.shape[0], _p(txt), txt.shape[0],
+                                      _p(emb), T, H, W, _p(vid_out), _p(txt_out))
+        if rc != 0:
+            raise RuntimeError(f"orc_block_forward failed: {rc}")
+        return vid_out, txt_out
+
+    def head(self, vid, txt, emb):
+        """qkv of both streams (seedvr2_dit_block.cpp:1141-1156)."""
+        vid, txt, emb = _f32(vid), _f32(txt), _f32(emb)
+        qv = np.zeros((vid.shape[0], 3 * self.dim), np.float32)
+        qt = np.zeros((txt.shape[0], 3 * self.dim), np.float32)
+        rc = load().orc_block_head(ctypes.byref(self.s), _p(vid), vid.shape[0], _p(txt), txt.shape[0], _p(emb),
+                                   _p(qv), _p(qt))
+        if rc != 0:
+            raise RuntimeError(f"orc_block_head failed: {rc}")
+        return qv, qt
+
+    def attention(self, qkv_v, qkv_t, T, H, W):
+        qkv_v, qkv_t = _f32(qkv_v), _f32(qkv_t)
+        av = np.zeros((qkv_v.shape[0], self.dim), np.float32)
+        at = np.zeros((qkv_t.shape[0], self.dim), np.float32)
+        rc = load().orc_block_attention(ctypes.byref(self.s), T, H, W, qkv_t.shape[0], _p(qkv_v), _p(qkv_t),
+                                        _p(av), _p(at))
+        if rc != 0:
+            raise RuntimeError(f"orc_block_attention failed: {rc}")
+        return av, at
+
+    def tail(self, att_v, att_t, vid, txt, emb):
+        """Outputs and the pre-gate projections from given attention outputs
+        (seedvr2_dit_block.cpp:1180-1260)."""
+        att_v, att_t, vid, txt, emb = map(_f32, (att_v, att_t, vid, txt, emb))
+        vo, to = np.zeros_like(vid), np.zeros_like(txt)
+        pv, pt = np.zeros_like(vid), np.zeros_like(txt)
+        rc = load().orc_block_tail(ctypes.byref(self.s), _p(att_v), att_v.shape[0], _p(att_t), att_t.shape[0],
+                                   _p(vid), _p(txt), _p(emb), _p(vo), _p(to), _p(pv), _p(pt))
+        if rc != 0:
+            raise RuntimeError(f"orc_block_tail failed: {rc}")
+        return vo, to, pv, pt
+
+
 def block_forward(weights, vid, txt, emb, T, H, W, *, dim, heads, head_dim=128, mlp_hidden,
                   eps=1e-5, shared=False, last_layer=False, shifted=False, wt=0, wh=0, ww=0,
                   rope_mode=ROPE_REFERENCE, theta=10000.0, qk_norm=True, threads=0):
     """weights: {"vid": {field: array}, "txt": {...} (unless shared), "freqs": [21]}."""
-    keep = []
-
-    def branch(d):
-        arrs = {k: _f32(d[k]) for k in BRANCH_FIELDS}
-        keep.append(arrs)
-        return OrcBranch(*[_p(arrs[k]) for k in BRANCH_FIELDS])
-
-    vb = branch(weights["vid"])
-    tb = vb if shared else branch(weights["txt"])
-    freqs = _f32(weights["freqs"])
-    blk = OrcBlock(dim, heads, head_dim, mlp_hidden, eps, int(shared), int(last_layer), int(shifted),
-                   wt, wh, ww, rope_mode, theta, int(qk_norm), vb, tb, _p(freqs), threads)
-    vid, txt, emb = _f32(vid), _f32(txt), _f32(emb)
-    vid_out = np.zeros_like(vid)
-    txt_out = np.zeros_like(txt)
-    rc = load().orc_block_forward(ctypes.byref(blk), _p(vid), vid.shape[0], _p(txt), txt.shape[0],
-                                  _p(emb), T, H, W, _p(vid_out), _p(txt_out))
-    if rc != 0:
-        raise RuntimeError(f"orc_block_forward failed: {rc}")
-    return vid_out, txt_out
+    blk = Block(weights, dim=dim, heads=heads, head_dim=head_dim, mlp_hidden=mlp_hidden, eps=eps, shared=shared,
+                last_layer=last_layer, shifted=shifted, wt=wt, wh=wh, ww=ww, rope_mode=rope_mode, theta=theta,
+                qk_norm=qk_norm, threads=threads)
+    return blk.forward(vid, txt, emb, T, H, W)

@@ -518,72 +518,91 @@ static int apply_mlp(const orc_block* blk, const orc_branch* br, const float* in
     return 0;
 }
 
-/* seedvr2_dit_block.cpp:1114-1267 */
-int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt,
-                      const float* emb, int T, int H, int W, float* vid_out, float* txt_out)
+/* Steps before the attention (seedvr2_dit_block.cpp:1141-1156): token
+ * RMSNorm + ada input (text skips the ada on the last layer), then the QKV
+ * InnerProducts.  qkv_v [Lv, 3D], qkv_t [Lt, 3D]. */
+int orc_block_head(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt, const float* emb,
+                   float* qkv_v, float* qkv_t)
 {
     const int D = blk->dim;
-    if (blk->heads * blk->head_dim != D || T * H * W != Lv || Lv <= 0 || Lt < 0)
+    if (blk->heads * blk->head_dim != D || Lv < 0 || Lt < 0)
         return -1;
     const orc_branch* vb = &blk->vid;
     const orc_branch* tb = blk->shared ? &blk->vid : &blk->txt; /* :1139 */
     const size_t nv = (size_t)Lv * D, nt = (size_t)Lt * D;
-    int rc = -100;
-
     float* xa_v = clone_rows(vid, nv);
     float* xa_t = clone_rows(txt, nt);
-    float* qkv_v = (float*)malloc(sizeof(float) * nv * 3);
-    float* qkv_t = (float*)malloc(sizeof(float) * (nt ? nt : 1) * 3);
-    float* att_v = (float*)malloc(sizeof(float) * nv);
-    float* att_t = (float*)malloc(sizeof(float) * (nt ? nt : 1));
-    float* p_v = (float*)malloc(sizeof(float) * nv);
-    float* p_t = (float*)malloc(sizeof(float) * (nt ? nt : 1));
-    float* m_in = (float*)malloc(sizeof(float) * (nv > nt ? nv : nt));
-    if (!xa_v || !xa_t || !qkv_v || !qkv_t || !att_v || !att_t || !p_v || !p_t || !m_in)
-        goto done;
-
-    /* :1141-1151 */
+    if (!xa_v || !xa_t)
+    {
+        free(xa_v);
+        free(xa_t);
+        return -100;
+    }
     orc_rmsnorm_rows(xa_v, Lv, D, blk->eps);
     orc_rmsnorm_rows(xa_t, Lt, D, blk->eps);
     orc_ada_input(xa_v, Lv, D, emb, vb->attn_shift, vb->attn_scale, 0);
     if (!blk->last_layer)
         orc_ada_input(xa_t, Lt, D, emb, tb->attn_shift, tb->attn_scale, 0);
-
-    /* :1155-1156 */
     orc_inner_product(xa_v, Lv, D, vb->w_qkv, NULL, 3 * D, qkv_v, blk->threads);
     orc_inner_product(xa_t, Lt, D, tb->w_qkv, NULL, 3 * D, qkv_t, blk->threads);
+    free(xa_v);
+    free(xa_t);
+    return 0;
+}
 
-    {
-        orc_attn_cfg cfg;
-        memset(&cfg, 0, sizeof(cfg));
-        cfg.heads = blk->heads;
-        cfg.head_dim = blk->head_dim;
-        cfg.eps = blk->eps;
-        cfg.qk_norm = blk->qk_norm;
-        cfg.rope_mode = blk->rope_mode;
-        cfg.freqs = blk->freqs;
-        cfg.rope_theta = blk->rope_theta;
-        cfg.gq_vid = vb->norm_q;
-        cfg.gk_vid = vb->norm_k;
-        cfg.gq_txt = tb->norm_q;
-        cfg.gk_txt = tb->norm_k;
-        cfg.shifted = blk->shifted;
-        cfg.wt = blk->wt;
-        cfg.wh = blk->wh;
-        cfg.ww = blk->ww;
-        cfg.threads = blk->threads;
-        const int arc = orc_window_attention(&cfg, T, H, W, Lt, qkv_v, qkv_t, att_v, att_t,
-                                             NULL, NULL, NULL, NULL, NULL);
-        if (arc != 0)
-        {
-            rc = arc == -1 ? -1 : -100;
-            goto done;
-        }
-    }
+/* The block's attention (seedvr2_dit_block.cpp:870-1091) with the block's
+ * parameters and the per-branch q/k norm weights. */
+int orc_block_attention(const orc_block* blk, int T, int H, int W, int Lt, const float* qkv_v, const float* qkv_t,
+                        float* att_v, float* att_t)
+{
+    const orc_branch* vb = &blk->vid;
+    const orc_branch* tb = blk->shared ? &blk->vid : &blk->txt;
+    orc_attn_cfg cfg;
+    memset(&cfg, 0, sizeof(cfg));
+    cfg.heads = blk->heads;
+    cfg.head_dim = blk->head_dim;
+    cfg.eps = blk->eps;
+    cfg.qk_norm = blk->qk_norm;
+    cfg.rope_mode = blk->rope_mode;
+    cfg.freqs = blk->freqs;
+    cfg.rope_theta = blk->rope_theta;
+    cfg.gq_vid = vb->norm_q;
+    cfg.gk_vid = vb->norm_k;
+    cfg.gq_txt = tb->norm_q;
+    cfg.gk_txt = tb->norm_k;
+    cfg.shifted = blk->shifted;
+    cfg.wt = blk->wt;
+    cfg.wh = blk->wh;
+    cfg.ww = blk->ww;
+    cfg.threads = blk->threads;
+    return orc_window_attention(&cfg, T, H, W, Lt, qkv_v, qkv_t, att_v, att_t, NULL, NULL, NULL, NULL, NULL);
+}
+
+/* Steps after the attention (seedvr2_dit_block.cpp:1180-1260): output
+ * projections with bias, gated residuals, the MLPs, and the last layer's
+ * text rule.  proj_v / proj_t (optional, may be NULL) receive the projected
+ * values before the gate, as the reference's debug capture (:1188-1192). */
+int orc_block_tail(const orc_block* blk, const float* att_v, int Lv, const float* att_t, int Lt, const float* vid,
+                   const float* txt, const float* emb, float* vid_out, float* txt_out, float* proj_v, float* proj_t)
+{
+    const int D = blk->dim;
+    const orc_branch* vb = &blk->vid;
+    const orc_branch* tb = blk->shared ? &blk->vid : &blk->txt;
+    const size_t nv = (size_t)Lv * D, nt = (size_t)Lt * D;
+    int rc = -100;
+    float* p_v = (float*)malloc(sizeof(float) * (nv ? nv : 1));
+    float* p_t = (float*)malloc(sizeof(float) * (nt ? nt : 1));
+    float* m_in = (float*)malloc(sizeof(float) * (nv > nt ? nv : (nt ? nt : 1)));
+    if (!p_v || !p_t || !m_in)
+        goto done;
 
     /* :1180-1209 */
     orc_inner_product(att_v, Lv, D, vb->w_proj, vb->b_proj, D, p_v, blk->threads);
     orc_inner_product(att_t, Lt, D, tb->w_proj, tb->b_proj, D, p_t, blk->threads);
+    if (proj_v)
+        memcpy(proj_v, p_v, sizeof(float) * nv);
+    if (proj_t && nt)
+        memcpy(proj_t, p_t, sizeof(float) * nt);
     orc_ada_output_residual(p_v, vid, Lv, D, emb, vb->attn_gate, 0);
     if (!blk->last_layer)
         orc_ada_output_residual(p_t, txt, Lt, D, emb, tb->attn_gate, 0);
@@ -605,7 +624,7 @@ int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const floa
         for (size_t i = 0; i < nt; i++)
             txt_out[i] = p_t[i] * 2.f;
     }
-    else
+    else if (Lt > 0)
     {
         /* :1248-1260 */
         memcpy(m_in, p_t, sizeof(float) * nt);
@@ -616,16 +635,41 @@ int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const floa
         orc_ada_output_residual(txt_out, p_t, Lt, D, emb, tb->mlp_gate, 3);
     }
     rc = 0;
-
 done:
-    free(xa_v);
-    free(xa_t);
+    free(p_v);
+    free(p_t);
+    free(m_in);
+    return rc;
+}
+
+/* seedvr2_dit_block.cpp:1114-1267 */
+int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt,
+                      const float* emb, int T, int H, int W, float* vid_out, float* txt_out)
+{
+    const int D = blk->dim;
+    if (blk->heads * blk->head_dim != D || T * H * W != Lv || Lv <= 0 || Lt < 0)
+        return -1;
+    const size_t nv = (size_t)Lv * D, nt = (size_t)Lt * D;
+    int rc = -100;
+    float* qkv_v = (float*)malloc(sizeof(float) * nv * 3);
+    float* qkv_t = (float*)malloc(sizeof(float) * (nt ? nt : 1) * 3);
+    float* att_v = (float*)malloc(sizeof(float) * nv);
+    float* att_t = (float*)malloc(sizeof(float) * (nt ? nt : 1));
+    if (!qkv_v || !qkv_t || !att_v || !att_t)
+        goto done;
+    if ((rc = orc_block_head(blk, vid, Lv, txt, Lt, emb, qkv_v, qkv_t)) != 0)
+        goto done;
+    rc = orc_block_attention(blk, T, H, W, Lt, qkv_v, qkv_t, att_v, att_t);
+    if (rc != 0)
+    {
+        rc = rc == -1 ? -1 : -100;
+        goto done;
+    }
+    rc = orc_block_tail(blk, att_v, Lv, att_t, Lt, vid, txt, emb, vid_out, txt_out, NULL, NULL);
+done:
     free(qkv_v);
     free(qkv_t);
     free(att_v);
     free(att_t);
-    free(p_v);
-    free(p_t);
-    free(m_in);
     return rc;
 }

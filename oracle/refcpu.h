@@ -151,6 +151,12 @@ typedef struct orc_block {
 
 /* One block forward (seedvr2_dit_block.cpp:1114-1267).  vid [Lv, D], txt [Lt, D],
  * emb [6D].  Returns 0, -1 on invalid shapes, -100 on allocation failure. */
+int orc_block_head(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt, const float* emb,
+                   float* qkv_v, float* qkv_t);
+int orc_block_attention(const orc_block* blk, int T, int H, int W, int Lt, const float* qkv_v, const float* qkv_t,
+                        float* att_v, float* att_t);
+int orc_block_tail(const orc_block* blk, const float* att_v, int Lv, const float* att_t, int Lt, const float* vid,
+                   const float* txt, const float* emb, float* vid_out, float* txt_out, float* proj_v, float* proj_t);
 int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt,
                       const float* emb, int T, int H, int W, float* vid_out, float* txt_out);
 

@@ -1,0 +1,704 @@
+// The SeedVR2DiTBlock layer on the device (src/layers/seedvr2_dit_block.{h,cpp}
+// of the reference): parameters, weight loading from the exported
+// .param/.bin pair, and the block forward as a chain of the library's kernels
+// on one stream — token RMSNorm + ada, the QKV / proj / MLP InnerProducts as
+// rocBLAS GEMMs, the windowed attention, gated residuals and SwiGLU.
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "ncnn_format.h"
+#include "sv2_internal.h"
+
+namespace
+{
+
+struct DevBranch
+{
+    const float* ada[6] = {};
+    const void* w_qkv = nullptr;
+    const void* w_proj = nullptr;
+    const float* b_proj = nullptr;
+    const float* norm_q = nullptr;
+    const float* norm_k = nullptr;
+    const void* w_gate = nullptr;
+    const void* w_in = nullptr;
+    const void* w_out = nullptr;
+};
+
+size_t dtype_size(int dtype)
+{
+    return dtype == SV2_F32 ? 4 : 2;
+}
+
+// One rocBLAS handle per device, shared by every block of the process.
+rocblas_handle blas_handle(int* rc)
+{
+    static std::mutex mutex;
+    static std::map<int, rocblas_handle> handles;
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess)
+    {
+        *rc = sv2::hip_error(err, "block: hipGetDevice");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mutex);
+    auto it = handles.find(device);
+    if (it != handles.end())
+        return it->second;
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success)
+    {
+        *rc = sv2::set_error(SV2_EDEVICE, "block: rocblas_create_handle failed");
+        return nullptr;
+    }
+    handles[device] = h;
+    return h;
+}
+
+// y[rows, out] = x[rows, in] W^T with W [out][in] row-major (the InnerProduct
+// of the reference without its bias), fp32 accumulation.
+int gemm_rows(rocblas_handle h, hipStream_t stream, int dtype, int rows, int in, int out, const void* x,
+              const void* w, void* y)
+{
+    if (rows == 0)
+        return SV2_OK;
+    const rocblas_datatype t = dtype == SV2_F32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
+    const float alpha = 1.f;
+    const float beta = 0.f;
+    rocblas_set_stream(h, stream);
+    // column-major view: Y^T [out x rows] = W [out x in] * X^T [in x rows]
+    const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, out, rows, in,
+                                              &alpha, w, t, in, x, t, in, &beta, y, t, out, y, t, out,
+                                              rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return sv2::set_error(SV2_EDEVICE, std::string("block: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+    return SV2_OK;
+}
+
+} // namespace
+
+struct sv2_block
+{
+    sv2_block_config cfg{};
+    int dtype = SV2_F32;
+    DevBranch vid;
+    DevBranch txt;
+    std::vector<void*> owned;
+    float freqs[21] = {};
+    bool has_freqs = false;
+    int T = 0, H = 0, W = 0;
+    bool shape_valid = false;
+    // RoPE table cache for the current rule and text length
+    float* rope = nullptr;
+    int rope_npos = 0;
+    int rope_key[5] = {-1, -1, -1, -1, -1};
+    // workspace kept by the block when the caller passes none
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    bool debug_on = false;
+    sv2_block_debug debug{};
+
+    ~sv2_block()
+    {
+        for (void* p : owned)
+            hipFree(p);
+        if (rope)
+            hipFree(rope);
+        if (ws)
+            hipFree(ws);
+    }
+};
+
+namespace
+{
+
+int validate_config(const sv2_block_config& c)
+{
+    if (c.dim <= 0 || c.heads <= 0 || c.head_dim <= 0 || c.mlp_hidden <= 0 || c.dim != c.heads * c.head_dim)
+        return sv2::set_error(SV2_EINVAL, "block: dim must equal heads * head_dim (SeedVR2DiTBlock::load_param)");
+    if (c.head_dim != 128)
+        return sv2::set_error(SV2_EUNSUPPORTED, "block: head_dim must be 128");
+    if (c.dim % 8 != 0 || c.mlp_hidden % 8 != 0 || c.dim > 4096)
+        return sv2::set_error(SV2_EUNSUPPORTED, "block: dim and mlp_hidden must be multiples of 8, dim <= 4096");
+    if (c.window_t < 0 || c.window_h < 0 || c.window_w < 0)
+        return sv2::set_error(SV2_EINVAL, "block: window extents must be >= 0");
+    if (c.rope_mode < SV2_ROPE_REFERENCE || c.rope_mode > SV2_ROPE_NONE)
+        return sv2::set_error(SV2_EINVAL, "block: unknown rope mode");
+    return SV2_OK;
+}
+
+// Uploads `count` elements: fp32 host values converted to `dtype` (matrices)
+// or kept fp32 (vectors, dtype SV2_F32).
+int upload(sv2_block* b, const float* host, size_t count, int dtype, const void** dev)
+{
+    void* p = nullptr;
+    const size_t bytes = count * dtype_size(dtype);
+    hipError_t err = hipMalloc(&p, bytes ? bytes : 4);
+    if (err != hipSuccess)
+        return sv2::hip_error(err, "block: hipMalloc of weights");
+    b->owned.push_back(p);
+    if (dtype == SV2_F32)
+    {
+        err = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
+    }
+    else
+    {
+        std::vector<_Float16> half(count);
+        for (size_t i = 0; i < count; i++)
+            half[i] = static_cast<_Float16>(host[i]);
+        err = hipMemcpy(p, half.data(), bytes, hipMemcpyHostToDevice);
+    }
+    if (err != hipSuccess)
+        return sv2::hip_error(err, "block: hipMemcpy of weights");
+    *dev = p;
+    return SV2_OK;
+}
+
+int bind_branch(sv2_block* b, const sv2_block_branch& in, bool on_device, DevBranch* out)
+{
+    const sv2_block_config& c = b->cfg;
+    const size_t D = c.dim, F = c.mlp_hidden, hd = c.head_dim;
+    for (int i = 0; i < 6; i++)
+        if (!in.ada[i])
+            return sv2::set_error(SV2_EINVAL, "block: missing ada vector");
+    if (!in.w_qkv || !in.w_proj || !in.b_proj || !in.norm_q || !in.norm_k || !in.w_gate || !in.w_in || !in.w_out)
+        return sv2::set_error(SV2_EINVAL, "block: missing branch weight");
+    if (on_device)
+    {
+        for (int i = 0; i < 6; i++)
+            out->ada[i] = static_cast<const float*>(in.ada[i]);
+        out->w_qkv = in.w_qkv;
+        out->w_proj = in.w_proj;
+        out->b_proj = static_cast<const float*>(in.b_proj);
+        out->norm_q = static_cast<const float*>(in.norm_q);
+        out->norm_k = static_cast<const float*>(in.norm_k);
+        out->w_gate = in.w_gate;
+        out->w_in = in.w_in;
+        out->w_out = in.w_out;
+        return SV2_OK;
+    }
+    int rc;
+    const void* p;
+    for (int i = 0; i < 6; i++)
+    {
+        if ((rc = upload(b, static_cast<const float*>(in.ada[i]), D, SV2_F32, &p)) != SV2_OK)
+            return rc;
+        out->ada[i] = static_cast<const float*>(p);
+    }
+    if ((rc = upload(b, static_cast<const float*>(in.w_qkv), 3 * D * D, b->dtype, &out->w_qkv)) != SV2_OK ||
+        (rc = upload(b, static_cast<const float*>(in.w_proj), D * D, b->dtype, &out->w_proj)) != SV2_OK ||
+        (rc = upload(b, static_cast<const float*>(in.w_gate), F * D, b->dtype, &out->w_gate)) != SV2_OK ||
+        (rc = upload(b, static_cast<const float*>(in.w_in), F * D, b->dtype, &out->w_in)) != SV2_OK ||
+        (rc = upload(b, static_cast<const float*>(in.w_out), D * F, b->dtype, &out->w_out)) != SV2_OK)
+        return rc;
+    if ((rc = upload(b, static_cast<const float*>(in.b_proj), D, SV2_F32, &p)) != SV2_OK)
+        return rc;
+    out->b_proj = static_cast<const float*>(p);
+    if ((rc = upload(b, static_cast<const float*>(in.norm_q), hd, SV2_F32, &p)) != SV2_OK)
+        return rc;
+    out->norm_q = static_cast<const float*>(p);
+    if ((rc = upload(b, static_cast<const float*>(in.norm_k), hd, SV2_F32, &p)) != SV2_OK)
+        return rc;
+    out->norm_k = static_cast<const float*>(p);
+    return SV2_OK;
+}
+
+sv2_window_rule block_rule(const sv2_block* b)
+{
+    sv2_window_rule r;
+    r.frames = b->T;
+    r.height = b->H;
+    r.width = b->W;
+    r.shifted = b->cfg.shifted_window ? 1 : 0;
+    r.wt = b->cfg.window_t;
+    r.wh = b->cfg.window_h;
+    r.ww = b->cfg.window_w;
+    return r;
+}
+
+// Builds (once per rule and text length) the RoPE cos/sin table on the device.
+int ensure_rope(sv2_block* b, int text_len, hipStream_t stream)
+{
+    if (b->cfg.rope_mode == SV2_ROPE_NONE)
+        return SV2_OK;
+    const int key[5] = {b->T, b->H, b->W, b->cfg.shifted_window, text_len};
+    if (b->rope && std::equal(key, key + 5, b->rope_key))
+        return SV2_OK;
+    const sv2_window_rule rule = block_rule(b);
+    const int npos = sv2_rope_positions_needed(&rule, text_len, b->cfg.rope_mode);
+    if (npos < 0)
+        return npos;
+    if (b->cfg.rope_mode == SV2_ROPE_REFERENCE && !b->has_freqs)
+        return sv2::set_error(SV2_EINVAL, "block: the reference RoPE needs rope_freqs");
+    std::vector<float> table(sv2_rope_table_floats(npos));
+    int rc = sv2_rope_table_build(b->cfg.rope_mode, b->freqs, 10000.f, npos, table.data());
+    if (rc != SV2_OK)
+        return rc;
+    if (b->rope && npos > b->rope_npos)
+    {
+        // the previous table may still be read by queued work
+        hipError_t err = hipStreamSynchronize(stream);
+        if (err != hipSuccess)
+            return sv2::hip_error(err, "block: synchronize before RoPE table resize");
+        hipFree(b->rope);
+        b->rope = nullptr;
+    }
+    if (!b->rope)
+    {
+        hipError_t err = hipMalloc(reinterpret_cast<void**>(&b->rope), table.size() * sizeof(float));
+        if (err != hipSuccess)
+        {
+            b->rope = nullptr;
+            return sv2::hip_error(err, "block: hipMalloc of the RoPE table");
+        }
+        b->rope_npos = npos;
+    }
+    hipError_t err = hipMemcpyAsync(b->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess)
+        err = hipStreamSynchronize(stream); // the host table goes out of scope
+    if (err != hipSuccess)
+        return sv2::hip_error(err, "block: RoPE table upload");
+    std::copy(key, key + 5, b->rope_key);
+    return SV2_OK;
+}
+
+sv2_attn_args attention_args(const sv2_block* b, int text_len)
+{
+    sv2_attn_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.rule = block_rule(b);
+    a.heads = b->cfg.heads;
+    a.head_dim = b->cfg.head_dim;
+    a.text_len = text_len;
+    a.eps = b->cfg.norm_eps;
+    a.qk_norm = b->cfg.qk_norm;
+    a.rope_mode = b->cfg.rope_mode;
+    a.rope_table = b->rope;
+    a.rope_npos = b->rope_npos;
+    a.qkv_dtype = b->dtype;
+    a.out_dtype = b->dtype;
+    const DevBranch& tb = b->cfg.shared_weights ? b->vid : b->txt;
+    a.gamma_q_vid = b->vid.norm_q;
+    a.gamma_k_vid = b->vid.norm_k;
+    a.gamma_q_txt = tb.norm_q;
+    a.gamma_k_txt = tb.norm_k;
+    return a;
+}
+
+// Workspace regions (bytes, 256-aligned): xa / m [R, D], qkv [R, 3D], att [R, D],
+// p_v [Lv, D], p_t [Lt, D], g and u [R, F], attention workspace; R = max(Lv, Lt).
+struct BlockWorkspace
+{
+    size_t xa, qkv_v, qkv_t, att_v, att_t, p_v, p_t, g, u, attn, total;
+};
+
+size_t align256(size_t v)
+{
+    return (v + 255) & ~static_cast<size_t>(255);
+}
+
+int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
+{
+    const size_t es = dtype_size(b->dtype);
+    const size_t D = b->cfg.dim, F = b->cfg.mlp_hidden;
+    const size_t Lv = static_cast<size_t>(b->T) * b->H * b->W, Lt = text_len;
+    const size_t R = std::max(Lv, Lt);
+    sv2_attn_args a = attention_args(b, text_len);
+    a.vid_qkv = reinterpret_cast<const void*>(16); // placeholders: the size query reads no memory
+    a.txt_qkv = reinterpret_cast<const void*>(16);
+    if (a.rope_mode != SV2_ROPE_NONE)
+    {
+        a.rope_table = reinterpret_cast<const float*>(16);
+        const sv2_window_rule rule = block_rule(b);
+        a.rope_npos = sv2_rope_positions_needed(&rule, text_len, a.rope_mode);
+        if (a.rope_npos < 0)
+            return a.rope_npos;
+    }
+    if (a.qk_norm && (!a.gamma_q_vid || !a.gamma_k_vid))
+        return sv2::set_error(SV2_EINVAL, "block: missing norm weights");
+    const int64_t attn = sv2_window_attention_workspace(&a);
+    if (attn < 0)
+        return static_cast<int>(attn);
+    size_t off = 0;
+    w->xa = off;
+    off = align256(off + R * D * es);
+    w->qkv_v = off;
+    off = align256(off + Lv * 3 * D * es);
+    w->qkv_t = off;
+    off = align256(off + Lt * 3 * D * es);
+    w->att_v = off;
+    off = align256(off + Lv * D * es);
+    w->att_t = off;
+    off = align256(off + Lt * D * es);
+    w->p_v = off;
+    off = align256(off + Lv * D * es);
+    w->p_t = off;
+    off = align256(off + Lt * D * es);
+    w->g = off;
+    off = align256(off + R * F * es);
+    w->u = off;
+    off = align256(off + R * F * es);
+    w->attn = off;
+    off = align256(off + static_cast<size_t>(attn));
+    w->total = off;
+    return SV2_OK;
+}
+
+// The MLP of one branch on rows [rows, D]: RMSNorm + ada (mlp shift/scale),
+// gate and in InnerProducts, SwiGLU, out InnerProduct, gated residual with x
+// (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).
+int branch_mlp(const sv2_block* b, rocblas_handle h, hipStream_t stream, const DevBranch& br, const float* emb,
+               const void* x, int rows, void* out, char* m, char* g, char* u)
+{
+    if (rows == 0)
+        return SV2_OK;
+    const int D = b->cfg.dim, F = b->cfg.mlp_hidden, dt = b->dtype;
+    int rc;
+    if ((rc = sv2_rmsnorm_ada(x, m, dt, rows, D, b->cfg.norm_eps, emb, br.ada[3], br.ada[4], 3, 1, stream)) != SV2_OK)
+        return rc;
+    if ((rc = gemm_rows(h, stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
+        (rc = gemm_rows(h, stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
+        return rc;
+    if ((rc = sv2_swiglu(g, u, dt, static_cast<int64_t>(rows) * F, stream)) != SV2_OK)
+        return rc;
+    if ((rc = gemm_rows(h, stream, dt, rows, F, D, g, br.w_out, out)) != SV2_OK)
+        return rc;
+    return sv2_ada_residual(out, x, dt, rows, D, emb, br.ada[5], 3, 0, stream);
+}
+
+} // namespace
+
+extern "C" {
+
+void sv2_block_config_default(sv2_block_config* c)
+{
+    if (!c)
+        return;
+    std::memset(c, 0, sizeof(*c));
+    c->dim = 2560;
+    c->heads = 20;
+    c->head_dim = 128;
+    c->mlp_hidden = 6912;
+    c->norm_eps = 1e-5f;
+    c->rope_mode = SV2_ROPE_REFERENCE;
+    c->qk_norm = 1;
+}
+
+int sv2_block_create(const sv2_block_config* config, const sv2_block_branch* vid, const sv2_block_branch* txt,
+                     const float* rope_freqs, int weights_on_device, int compute_dtype, sv2_block** out)
+{
+    using namespace sv2;
+    if (!config || !vid || !out || (!config->shared_weights && !txt))
+        return set_error(SV2_EINVAL, "sv2_block_create: null argument");
+    *out = nullptr;
+    int rc = validate_config(*config);
+    if (rc != SV2_OK)
+        return rc;
+    if (compute_dtype != SV2_F32 && compute_dtype != SV2_F16)
+        return set_error(SV2_EINVAL, "sv2_block_create: compute dtype must be SV2_F32 or SV2_F16");
+    sv2_block* b = new sv2_block();
+    b->cfg = *config;
+    b->dtype = compute_dtype;
+    if (rope_freqs)
+    {
+        std::memcpy(b->freqs, rope_freqs, sizeof(b->freqs));
+        b->has_freqs = true;
+    }
+    if ((rc = bind_branch(b, *vid, weights_on_device != 0, &b->vid)) == SV2_OK && !config->shared_weights)
+        rc = bind_branch(b, *txt, weights_on_device != 0, &b->txt);
+    if (rc != SV2_OK)
+    {
+        delete b;
+        return rc;
+    }
+    if (config->shared_weights)
+        b->txt = b->vid;
+    *out = b;
+    return SV2_OK;
+}
+
+int sv2_block_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_block** out)
+{
+    using namespace sv2;
+    if (!param_path || !bin_path || !out)
+        return set_error(SV2_EINVAL, "sv2_block_load: null argument");
+    *out = nullptr;
+    std::vector<ParamLayer> layers;
+    std::string err;
+    if (read_param_file(param_path, &layers, &err) != 0)
+        return set_error(SV2_EINVAL, "sv2_block_load: " + err);
+    const ParamLayer* layer = nullptr;
+    for (const ParamLayer& l : layers)
+        if (l.type == "SeedVR2DiTBlock")
+            layer = &l;
+    if (!layer)
+        return set_error(SV2_EINVAL, std::string("sv2_block_load: no SeedVR2DiTBlock layer in ") + param_path);
+    if (layer->bottoms.size() != 4 || layer->tops.size() != 2)
+        return set_error(SV2_EINVAL, "sv2_block_load: SeedVR2DiTBlock needs 4 bottoms and 2 tops");
+    sv2_block_config c;
+    sv2_block_config_default(&c);
+    c.block_index = layer->get_int(0, 0);
+    c.shared_weights = layer->get_int(1, 0) != 0;
+    c.last_layer = layer->get_int(2, 0) != 0;
+    c.shifted_window = layer->get_int(3, 0) != 0;
+    c.dim = layer->get_int(4, 2560);
+    c.heads = layer->get_int(5, 20);
+    c.head_dim = layer->get_int(6, 128);
+    c.mlp_hidden = layer->get_int(7, 6912);
+    c.norm_eps = layer->get_float(8, 1e-5f);
+    c.window_t = layer->get_int(9, 0);
+    c.window_h = layer->get_int(10, 0);
+    c.window_w = layer->get_int(11, 0);
+    c.rope_mode = layer->get_int(12, SV2_ROPE_REFERENCE);
+    c.qk_norm = layer->get_int(13, 1) != 0;
+    int rc = validate_config(c);
+    if (rc != SV2_OK)
+        return rc;
+
+    // weight order of load_branch / load_model (seedvr2_dit_block.cpp:657-688)
+    BinReader bin;
+    if (bin.open(bin_path, &err) != 0)
+        return set_error(SV2_EDEVICE, "sv2_block_load: " + err);
+    const size_t D = c.dim, F = c.mlp_hidden, hd = c.head_dim;
+    struct HostBranch
+    {
+        std::vector<float> ada[6], w_qkv, w_proj, b_proj, norm_q, norm_k, w_gate, w_in, w_out;
+    };
+    HostBranch hb[2];
+    const int nbranch = c.shared_weights ? 1 : 2;
+    for (int bi = 0; bi < nbranch; bi++)
+    {
+        HostBranch& h = hb[bi];
+        bool ok = true;
+        for (int i = 0; i < 6 && ok; i++)
+            ok = bin.load_raw(D, &h.ada[i], &err) == 0;
+        ok = ok && bin.load_tagged(3 * D * D, &h.w_qkv, &err) == 0;
+        ok = ok && bin.load_tagged(D * D, &h.w_proj, &err) == 0;
+        ok = ok && bin.load_raw(D, &h.b_proj, &err) == 0;
+        ok = ok && bin.load_raw(hd, &h.norm_q, &err) == 0;
+        ok = ok && bin.load_raw(hd, &h.norm_k, &err) == 0;
+        ok = ok && bin.load_tagged(F * D, &h.w_gate, &err) == 0;
+        ok = ok && bin.load_tagged(F * D, &h.w_in, &err) == 0;
+        ok = ok && bin.load_tagged(D * F, &h.w_out, &err) == 0;
+        if (!ok)
+            return set_error(SV2_EDEVICE, std::string("sv2_block_load: ") + bin_path + ": " + err);
+    }
+    std::vector<float> freqs;
+    if (bin.load_raw(21, &freqs, &err) != 0)
+        return set_error(SV2_EDEVICE, std::string("sv2_block_load: ") + bin_path + ": rope freqs: " + err);
+    auto view = [](const HostBranch& h) {
+        sv2_block_branch v;
+        for (int i = 0; i < 6; i++)
+            v.ada[i] = h.ada[i].data();
+        v.w_qkv = h.w_qkv.data();
+        v.w_proj = h.w_proj.data();
+        v.b_proj = h.b_proj.data();
+        v.norm_q = h.norm_q.data();
+        v.norm_k = h.norm_k.data();
+        v.w_gate = h.w_gate.data();
+        v.w_in = h.w_in.data();
+        v.w_out = h.w_out.data();
+        return v;
+    };
+    const sv2_block_branch vb = view(hb[0]);
+    const sv2_block_branch tb = view(hb[nbranch - 1]);
+    return sv2_block_create(&c, &vb, &tb, freqs.data(), 0, compute_dtype, out);
+}
+
+int sv2_block_get_config(const sv2_block* block, sv2_block_config* config)
+{
+    if (!block || !config)
+        return sv2::set_error(SV2_EINVAL, "sv2_block_get_config: null argument");
+    *config = block->cfg;
+    return SV2_OK;
+}
+
+int sv2_block_set_runtime_shape(sv2_block* block, int frames, int height, int width)
+{
+    if (!block)
+        return sv2::set_error(SV2_EINVAL, "sv2_block_set_runtime_shape: null block");
+    block->T = frames;
+    block->H = height;
+    block->W = width;
+    block->shape_valid = frames > 0 && height > 0 && width > 0;
+    return block->shape_valid ? SV2_OK : sv2::set_error(SV2_EINVAL, "sv2_block_set_runtime_shape: bad shape");
+}
+
+int64_t sv2_block_workspace_size(const sv2_block* block, int text_len)
+{
+    using namespace sv2;
+    if (!block || text_len < 0)
+        return set_error(SV2_EINVAL, "sv2_block_workspace_size: bad argument");
+    if (!block->shape_valid)
+        return set_error(SV2_EINVAL, "sv2_block_workspace_size: runtime shape not set");
+    BlockWorkspace w;
+    const int rc = workspace_layout(block, text_len, &w);
+    return rc == SV2_OK ? static_cast<int64_t>(w.total) : rc;
+}
+
+int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_len, const float* emb, void* vid_out,
+                      void* txt_out, void* workspace, size_t workspace_bytes, void* stream_ptr)
+{
+    using namespace sv2;
+    if (!b || !vid || !emb || !vid_out || text_len < 0 || (text_len > 0 && (!txt || !txt_out)))
+        return set_error(SV2_EINVAL, "sv2_block_forward: null argument or bad text length");
+    if (!b->shape_valid)
+        return set_error(SV2_EINVAL, "sv2_block_forward: set_runtime_shape was not called");
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    BlockWorkspace w;
+    int rc = workspace_layout(b, text_len, &w);
+    if (rc != SV2_OK)
+        return rc;
+    char* ws = static_cast<char*>(workspace);
+    if (ws)
+    {
+        if (workspace_bytes < w.total)
+            return set_error(SV2_EINVAL, "sv2_block_forward: workspace too small");
+    }
+    else
+    {
+        if (b->ws_bytes < w.total)
+        {
+            if (b->ws)
+            {
+                hipError_t err = hipStreamSynchronize(stream); // queued work may still use the old buffer
+                if (err != hipSuccess)
+                    return hip_error(err, "sv2_block_forward: synchronize before workspace resize");
+                hipFree(b->ws);
+                b->ws = nullptr;
+                b->ws_bytes = 0;
+            }
+            hipError_t err = hipMalloc(&b->ws, w.total);
+            if (err != hipSuccess)
+            {
+                b->ws = nullptr;
+                return hip_error(err, "sv2_block_forward: workspace allocation");
+            }
+            b->ws_bytes = w.total;
+        }
+        ws = static_cast<char*>(b->ws);
+    }
+    if ((rc = ensure_rope(b, text_len, stream)) != SV2_OK)
+        return rc;
+    rocblas_handle h = blas_handle(&rc);
+    if (!h)
+        return rc;
+
+    const sv2_block_config& c = b->cfg;
+    const int D = c.dim, dt = b->dtype;
+    const int Lv = b->T * b->H * b->W, Lt = text_len;
+    const DevBranch& vb = b->vid;
+    const DevBranch& tb = c.shared_weights ? b->vid : b->txt;
+    char* xa = ws + w.xa;
+    char* qkv_v = ws + w.qkv_v;
+    char* qkv_t = ws + w.qkv_t;
+    char* att_v = ws + w.att_v;
+    char* att_t = ws + w.att_t;
+    char* p_v = ws + w.p_v;
+    char* p_t = ws + w.p_t;
+    char* g = ws + w.g;
+    char* u = ws + w.u;
+    const size_t es = dtype_size(dt);
+
+    // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
+    if ((rc = sv2_rmsnorm_ada(vid, xa, dt, Lv, D, c.norm_eps, emb, vb.ada[0], vb.ada[1], 0, 1, stream)) != SV2_OK)
+        return rc;
+    if ((rc = gemm_rows(h, stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
+        return rc;
+    const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
+    auto capture = [&](float* dst, const void* src, int rows, int cols) {
+        return dst ? launch_to_f32(dst, src, dt, static_cast<long long>(rows) * cols, stream) : SV2_OK;
+    };
+    if (dbg && (rc = capture(dbg->qkv_vid, qkv_v, Lv, 3 * D)) != SV2_OK)
+        return rc;
+    if (Lt > 0)
+    {
+        if ((rc = sv2_rmsnorm_ada(txt, xa, dt, Lt, D, c.norm_eps, emb, tb.ada[0], tb.ada[1], 0, c.last_layer ? 0 : 1,
+                                  stream)) != SV2_OK)
+            return rc;
+        if ((rc = gemm_rows(h, stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
+            return rc;
+        if (dbg && (rc = capture(dbg->qkv_txt, qkv_t, Lt, 3 * D)) != SV2_OK)
+            return rc;
+    }
+    // windowed joint attention (:870-1091)
+    sv2_attn_args a = attention_args(b, text_len);
+    a.vid_qkv = qkv_v;
+    a.txt_qkv = Lt > 0 ? qkv_t : nullptr;
+    a.vid_out = att_v;
+    a.txt_out = Lt > 0 ? att_t : nullptr;
+    a.workspace = ws + w.attn;
+    a.workspace_bytes = w.total - w.attn;
+    if ((rc = sv2_window_attention(&a, stream)) != SV2_OK)
+        return rc;
+    if (dbg && ((rc = capture(dbg->attention_vid, att_v, Lv, D)) != SV2_OK ||
+                (Lt > 0 && (rc = capture(dbg->attention_txt, att_t, Lt, D)) != SV2_OK)))
+        return rc;
+    // output projections with bias, gated residuals (:1180-1209)
+    if ((rc = gemm_rows(h, stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK ||
+        (rc = launch_bias_rows(p_v, vb.b_proj, dt, Lv, D, stream)) != SV2_OK)
+        return rc;
+    if (dbg && (rc = capture(dbg->projected_vid, p_v, Lv, D)) != SV2_OK)
+        return rc;
+    if ((rc = sv2_ada_residual(p_v, vid, dt, Lv, D, emb, vb.ada[2], 0, 0, stream)) != SV2_OK)
+        return rc;
+    if (Lt > 0)
+    {
+        if ((rc = gemm_rows(h, stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK ||
+            (rc = launch_bias_rows(p_t, tb.b_proj, dt, Lt, D, stream)) != SV2_OK)
+            return rc;
+        if (dbg && (rc = capture(dbg->projected_txt, p_t, Lt, D)) != SV2_OK)
+            return rc;
+        rc = c.last_layer ? sv2_ada_residual(p_t, txt, dt, Lt, D, nullptr, nullptr, 0, 1, stream)
+                          : sv2_ada_residual(p_t, txt, dt, Lt, D, emb, tb.ada[2], 0, 0, stream);
+        if (rc != SV2_OK)
+            return rc;
+    }
+    // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)
+    if ((rc = branch_mlp(b, h, stream, vb, emb, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
+        return rc;
+    if (Lt > 0)
+    {
+        if (c.last_layer)
+        {
+            hipError_t err = hipMemcpyAsync(txt_out, p_t, static_cast<size_t>(Lt) * D * es, hipMemcpyDeviceToDevice,
+                                            stream);
+            if (err != hipSuccess)
+                return hip_error(err, "sv2_block_forward: text copy");
+            if ((rc = sv2_ada_residual(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 0, 2, stream)) != SV2_OK)
+                return rc;
+        }
+        else if ((rc = branch_mlp(b, h, stream, tb, emb, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
+        {
+            return rc;
+        }
+    }
+    if (dbg && ((rc = capture(dbg->output_vid, vid_out, Lv, D)) != SV2_OK ||
+                (Lt > 0 && (rc = capture(dbg->output_txt, txt_out, Lt, D)) != SV2_OK)))
+        return rc;
+    return SV2_OK;
+}
+
+int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug)
+{
+    if (!block)
+        return sv2::set_error(SV2_EINVAL, "sv2_block_set_debug: null block");
+    block->debug_on = debug != nullptr;
+    if (debug)
+        block->debug = *debug;
+    return SV2_OK;
+}
+
+void sv2_block_destroy(sv2_block* block)
+{
+    delete block;
+}
+
+} // extern "C"

@@ -3,6 +3,7 @@
 // the SwiGLU gate.  All three are HBM-bound; they move 16 bytes per lane per
 // access (8 halfs or 4+4 floats) and read every element once.
 #include "sv2_internal.h"
+#include "vec_io.h"
 
 #include <cmath>
 
@@ -11,90 +12,7 @@ namespace sv2
 namespace
 {
 
-struct F32
-{
-};
-struct F16
-{
-};
-struct BF16
-{
-};
-
-template <typename T>
-__device__ inline void ld8(const void* base, long long i, float x[8]);
-template <typename T>
-__device__ inline void st8(void* base, long long i, const float x[8]);
-
-template <>
-__device__ inline void ld8<F32>(const void* base, long long i, float x[8])
-{
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-    const float4 a = p[0];
-    const float4 b = p[1];
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-template <>
-__device__ inline void st8<F32>(void* base, long long i, const float x[8])
-{
-    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + i);
-    p[0] = make_float4(x[0], x[1], x[2], x[3]);
-    p[1] = make_float4(x[4], x[5], x[6], x[7]);
-}
-
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-
-template <>
-__device__ inline void ld8<F16>(const void* base, long long i, float x[8])
-{
-    const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(base) + i);
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        x[e] = static_cast<float>(v[e]);
-}
-template <>
-__device__ inline void st8<F16>(void* base, long long i, const float x[8])
-{
-    f16x8 v;
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        v[e] = static_cast<_Float16>(x[e]);
-    *reinterpret_cast<f16x8*>(static_cast<_Float16*>(base) + i) = v;
-}
-
-// float -> bf16 with round-to-nearest-even (NaN kept quiet).
-__device__ inline uint32_t to_bf16_bits(float f)
-{
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7fffffffu) > 0x7f800000u)
-        return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-
-template <>
-__device__ inline void ld8<BF16>(const void* base, long long i, float x[8])
-{
-    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-    {
-        x[2 * e] = __builtin_bit_cast(float, w[e] << 16);
-        x[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
-    }
-}
-template <>
-__device__ inline void st8<BF16>(void* base, long long i, const float x[8])
-{
-    uint4 v;
-    v.x = to_bf16_bits(x[0]) | (to_bf16_bits(x[1]) << 16);
-    v.y = to_bf16_bits(x[2]) | (to_bf16_bits(x[3]) << 16);
-    v.z = to_bf16_bits(x[4]) | (to_bf16_bits(x[5]) << 16);
-    v.w = to_bf16_bits(x[6]) | (to_bf16_bits(x[7]) << 16);
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + i) = v;
-}
+using namespace vec;
 
 // Most 8-element vectors one lane keeps in registers per row (dim <= 8*64*kMaxVec).
 constexpr int kMaxVec = 8;
@@ -103,12 +21,14 @@ constexpr int kMaxVec = 8;
 // (seedvr2_dit_block.cpp:770-805): a double sum of squares, inv =
 // 1/sqrtf(float(ss/dim) + eps), x *= inv, then
 // x = x*(emb[c*6+slot+1] + scale[c]) + emb[c*6+slot] + shift[c] evaluated left
-// to right in fp32 with no fused multiply-add.  The row stays in registers
+// to right in fp32 with no fused multiply-add.  With `gamma` (the DiT output
+// head's norm weight, seedvr2_dit_output.cpp:372-384) x = (x * inv) * gamma[c]
+// before the modulation.  The row stays in registers
 // between the reduction and the write, so HBM sees one read and one write.
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y, int rows, int dim, float eps,
                                                           const float* emb, const float* shift, const float* scale,
-                                                          int slot, int has_ada)
+                                                          const float* gamma, int slot, int has_ada)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -147,6 +67,8 @@ __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y
             {
                 const int c = vi * 8 + e;
                 float t = v[k][e] * inv;
+                if (gamma)
+                    t = t * gamma[c];
                 if (has_ada)
                 {
                     const float mul = emb[c * 6 + slot + 1] + scale[c];
@@ -226,12 +148,109 @@ __global__ __launch_bounds__(256) void swiglu_kernel(void* gate, const void* val
     st8<T>(gate, i, g);
 }
 
+// y[r][c] += b[c] (the bias of an InnerProduct whose matrix product ran
+// without one), optionally followed by silu(v) = v / (1 + exp(-v)) (the time
+// MLP of the DiT input head, seedvr2_dit_input.cpp:377-388).
+template <typename T>
+__global__ __launch_bounds__(256) void bias_rows_kernel(void* y, const float* b, long long count, int cols,
+                                                        int silu)
+{
+#pragma clang fp contract(off)
+    const long long i = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i >= count)
+        return;
+    float a[8];
+    ld8<T>(y, i, a);
+    const int c0 = static_cast<int>(i % cols);
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+    {
+        a[e] += b[c0 + e];
+        if (silu)
+            a[e] = a[e] / (1.f + expf(-a[e]));
+    }
+    st8<T>(y, i, a);
+}
+
+// dst (fp32) = src (dtype), 8 elements per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void to_f32_kernel(float* dst, const void* src, long long count)
+{
+    const long long i = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i >= count)
+        return;
+    float a[8];
+    ld8<T>(src, i, a);
+    st8<F32>(dst, i, a);
+}
+
 bool dtype_ok(int t)
 {
     return t == SV2_F32 || t == SV2_F16 || t == SV2_BF16;
 }
 
 } // namespace
+
+int launch_bias_rows(void* y, const float* b, int dtype, int rows, int cols, hipStream_t stream)
+{
+    return launch_bias_act(y, b, dtype, rows, cols, 0, stream);
+}
+
+int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int silu, hipStream_t stream)
+{
+    if (!dtype_ok(dtype) || rows < 0 || cols <= 0 || cols % 8 != 0)
+        return set_error(SV2_EINVAL, "bias_rows: bad dtype or shape");
+    const long long count = static_cast<long long>(rows) * cols;
+    if (count == 0)
+        return SV2_OK;
+    const dim3 grid(static_cast<unsigned>((count / 8 + 255) / 256));
+    if (dtype == SV2_F32)
+        hipLaunchKernelGGL(bias_rows_kernel<F32>, grid, dim3(256), 0, stream, y, b, count, cols, silu);
+    else if (dtype == SV2_F16)
+        hipLaunchKernelGGL(bias_rows_kernel<F16>, grid, dim3(256), 0, stream, y, b, count, cols, silu);
+    else
+        hipLaunchKernelGGL(bias_rows_kernel<BF16>, grid, dim3(256), 0, stream, y, b, count, cols, silu);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "bias_rows_kernel launch");
+}
+int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipStream_t stream)
+{
+    if (!dtype_ok(dtype) || count < 0 || count % 8 != 0)
+        return set_error(SV2_EINVAL, "to_f32: bad dtype or count");
+    if (count == 0)
+        return SV2_OK;
+    if (dtype == SV2_F32)
+    {
+        const hipError_t err = hipMemcpyAsync(dst, src, count * sizeof(float), hipMemcpyDeviceToDevice, stream);
+        return err == hipSuccess ? SV2_OK : hip_error(err, "to_f32 copy");
+    }
+    const dim3 grid(static_cast<unsigned>((count / 8 + 255) / 256));
+    if (dtype == SV2_F16)
+        hipLaunchKernelGGL(to_f32_kernel<F16>, grid, dim3(256), 0, stream, dst, src, count);
+    else
+        hipLaunchKernelGGL(to_f32_kernel<BF16>, grid, dim3(256), 0, stream, dst, src, count);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "to_f32_kernel launch");
+}
+int launch_rmsnorm_ada(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* emb,
+                       const float* shift, const float* scale, const float* gamma, int slot_base, int has_ada,
+                       hipStream_t stream)
+{
+    if (rows == 0)
+        return SV2_OK;
+    const dim3 grid((rows + 3) / 4);
+    if (dtype == SV2_F32)
+        hipLaunchKernelGGL(rmsnorm_ada_kernel<F32>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
+                           gamma, slot_base, has_ada);
+    else if (dtype == SV2_F16)
+        hipLaunchKernelGGL(rmsnorm_ada_kernel<F16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
+                           gamma, slot_base, has_ada);
+    else
+        hipLaunchKernelGGL(rmsnorm_ada_kernel<BF16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift,
+                           scale, gamma, slot_base, has_ada);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
+}
 } // namespace sv2
 
 extern "C" {
@@ -250,19 +269,8 @@ int sv2_rmsnorm_ada(const void* x, void* y, int io_dtype, int rows, int dim, flo
         return set_error(SV2_EINVAL, "rmsnorm_ada: null pointer");
     if (slot_base != 0 && slot_base != 3)
         return set_error(SV2_EINVAL, "rmsnorm_ada: slot_base must be 0 or 3");
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const dim3 grid((rows + 3) / 4);
-    if (io_dtype == SV2_F32)
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<F32>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
-                           slot_base, has_ada);
-    else if (io_dtype == SV2_F16)
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<F16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
-                           slot_base, has_ada);
-    else
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<BF16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift,
-                           scale, slot_base, has_ada);
-    const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
+    return launch_rmsnorm_ada(x, y, io_dtype, rows, dim, eps, emb, shift, scale, nullptr, slot_base, has_ada,
+                              static_cast<hipStream_t>(stream_ptr));
 }
 
 int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int dim, const float* emb,

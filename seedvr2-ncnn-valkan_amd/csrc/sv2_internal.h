@@ -105,4 +105,18 @@ int hip_error(hipError_t err, const char* what);
 // Builds the closed-form plan; returns SV2_OK or an error code.
 int build_plan(const sv2_window_rule& rule, PlanArgs* plan);
 
+// y[r][c] += b[c] for a [rows, cols] tensor of dtype (cols a multiple of 8).
+int launch_bias_rows(void* y, const float* b, int dtype, int rows, int cols, hipStream_t stream);
+// The same, then y = silu(y) when `silu` is non-zero.
+int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int silu, hipStream_t stream);
+
+// Token RMSNorm (optionally times gamma[c]) and ada modulation; the
+// arguments of sv2_rmsnorm_ada, already validated, plus `gamma` (may be NULL).
+int launch_rmsnorm_ada(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* emb,
+                       const float* shift, const float* scale, const float* gamma, int slot_base, int has_ada,
+                       hipStream_t stream);
+
+// dst (fp32) = src (dtype); count a multiple of 8.
+int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipStream_t stream);
+
 } // namespace sv2

@@ -36,6 +36,15 @@ EXPORTS = [
     "sv2_rmsnorm_ada",
     "sv2_ada_residual",
     "sv2_swiglu",
+    "sv2_block_config_default",
+    "sv2_block_load",
+    "sv2_block_create",
+    "sv2_block_get_config",
+    "sv2_block_set_runtime_shape",
+    "sv2_block_workspace_size",
+    "sv2_block_forward",
+    "sv2_block_destroy",
+    "sv2_block_set_debug",
     "sv2_last_error",
     "sv2_version",
 ]
@@ -84,6 +93,52 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class BlockConfig(ctypes.Structure):
+    _fields_ = [
+        ("block_index", ctypes.c_int),
+        ("shared_weights", ctypes.c_int),
+        ("last_layer", ctypes.c_int),
+        ("shifted_window", ctypes.c_int),
+        ("dim", ctypes.c_int),
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("mlp_hidden", ctypes.c_int),
+        ("norm_eps", ctypes.c_float),
+        ("window_t", ctypes.c_int),
+        ("window_h", ctypes.c_int),
+        ("window_w", ctypes.c_int),
+        ("rope_mode", ctypes.c_int),
+        ("qk_norm", ctypes.c_int),
+    ]
+
+
+# Branch weights in the exporter's order (ada vectors first).
+BRANCH_FIELDS = ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate",
+                 "w_qkv", "w_proj", "b_proj", "norm_q", "norm_k", "w_gate", "w_in", "w_out")
+
+
+class BlockBranch(ctypes.Structure):
+    _fields_ = [
+        ("ada", ctypes.c_void_p * 6),
+        ("w_qkv", ctypes.c_void_p),
+        ("w_proj", ctypes.c_void_p),
+        ("b_proj", ctypes.c_void_p),
+        ("norm_q", ctypes.c_void_p),
+        ("norm_k", ctypes.c_void_p),
+        ("w_gate", ctypes.c_void_p),
+        ("w_in", ctypes.c_void_p),
+        ("w_out", ctypes.c_void_p),
+    ]
+
+
+BLOCK_DEBUG_FIELDS = ("qkv_vid", "qkv_txt", "attention_vid", "attention_txt", "projected_vid", "projected_txt",
+                      "output_vid", "output_txt")
+
+
+class BlockDebug(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in BLOCK_DEBUG_FIELDS]
+
+
 _lib = None
 
 
@@ -120,6 +175,26 @@ def load() -> ctypes.CDLL:
     lib.sv2_ada_residual.restype = i
     lib.sv2_swiglu.argtypes = [vp, vp, i, ctypes.c_int64, vp]
     lib.sv2_swiglu.restype = i
+    cfgp = ctypes.POINTER(BlockConfig)
+    brp = ctypes.POINTER(BlockBranch)
+    lib.sv2_block_config_default.argtypes = [cfgp]
+    lib.sv2_block_config_default.restype = None
+    lib.sv2_block_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i, ctypes.POINTER(vp)]
+    lib.sv2_block_load.restype = i
+    lib.sv2_block_create.argtypes = [cfgp, brp, brp, vp, i, i, ctypes.POINTER(vp)]
+    lib.sv2_block_create.restype = i
+    lib.sv2_block_get_config.argtypes = [vp, cfgp]
+    lib.sv2_block_get_config.restype = i
+    lib.sv2_block_set_runtime_shape.argtypes = [vp, i, i, i]
+    lib.sv2_block_set_runtime_shape.restype = i
+    lib.sv2_block_workspace_size.argtypes = [vp, i]
+    lib.sv2_block_workspace_size.restype = ctypes.c_int64
+    lib.sv2_block_forward.argtypes = [vp, vp, vp, i, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.sv2_block_forward.restype = i
+    lib.sv2_block_set_debug.argtypes = [vp, ctypes.POINTER(BlockDebug)]
+    lib.sv2_block_set_debug.restype = i
+    lib.sv2_block_destroy.argtypes = [vp]
+    lib.sv2_block_destroy.restype = None
     lib.sv2_last_error.argtypes = []
     lib.sv2_last_error.restype = ctypes.c_char_p
     lib.sv2_version.argtypes = []
@@ -279,3 +354,153 @@ def ada_residual(x, residual, emb=None, gate=None, slot_base=0, mode=0, stream=N
 def swiglu(gate, value, stream=None):
     check(load().sv2_swiglu(_ptr(gate), _ptr(value), torch_dtype_code(gate), gate.numel(),
                             _stream(stream)), "sv2_swiglu")
+
+
+def block_config(**overrides) -> BlockConfig:
+    """The reference defaults (block 0 of SeedVR2-3B) with fields replaced."""
+    c = BlockConfig()
+    load().sv2_block_config_default(ctypes.byref(c))
+    for k, v in overrides.items():
+        if not hasattr(c, k):
+            raise KeyError(k)
+        setattr(c, k, v)
+    return c
+
+
+def _branch_struct(ptrs: dict) -> BlockBranch:
+    b = BlockBranch()
+    for i, name in enumerate(BRANCH_FIELDS[:6]):
+        b.ada[i] = ptrs[name]
+    for name in BRANCH_FIELDS[6:]:
+        setattr(b, name, ptrs[name])
+    return b
+
+
+class DitBlock:
+    """One SeedVR2DiTBlock on the device (sv2_block_* of the C ABI).
+
+    Construct with `DitBlock.load(param, bin, dtype)` (an exported block) or
+    `DitBlock.from_host(config, weights, dtype)` (numpy fp32 weights:
+    {"vid": {field: array}, "txt": {...}, "freqs": [21]}) or
+    `DitBlock.from_device(config, weights, dtype)` (torch device tensors,
+    matrices in the compute dtype, vectors fp32; borrowed)."""
+
+    def __init__(self, handle: int, dtype: int, keep=None):
+        self._h = ctypes.c_void_p(handle)
+        self.dtype = dtype
+        self._keep = keep
+        self.config = BlockConfig()
+        check(load().sv2_block_get_config(self._h, ctypes.byref(self.config)), "sv2_block_get_config")
+
+    @classmethod
+    def load(cls, param_path, bin_path, dtype=F32) -> "DitBlock":
+        h = ctypes.c_void_p()
+        check(load().sv2_block_load(str(param_path).encode(), str(bin_path).encode(), dtype,
+                                    ctypes.byref(h)), "sv2_block_load")
+        return cls(h.value, dtype)
+
+    @classmethod
+    def _create(cls, config, weights, dtype, on_device, ptr_of) -> "DitBlock":
+        keep = []
+
+        def branch(d):
+            ptrs = {}
+            for name in BRANCH_FIELDS:
+                arr, p = ptr_of(d[name])
+                keep.append(arr)
+                ptrs[name] = p
+            return _branch_struct(ptrs)
+
+        vb = branch(weights["vid"])
+        tb = vb if config.shared_weights else branch(weights["txt"])
+        freqs = None
+        if weights.get("freqs") is not None:
+            freqs = np.ascontiguousarray(np.asarray(weights["freqs"], dtype=np.float32).reshape(-1))
+            keep.append(freqs)
+        h = ctypes.c_void_p()
+        check(load().sv2_block_create(ctypes.byref(config), ctypes.byref(vb), ctypes.byref(tb),
+                                      None if freqs is None else freqs.ctypes.data, int(on_device), dtype,
+                                      ctypes.byref(h)), "sv2_block_create")
+        return cls(h.value, dtype, keep if on_device else None)
+
+    @classmethod
+    def from_host(cls, config, weights, dtype=F32) -> "DitBlock":
+        def ptr_of(a):
+            arr = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+            return arr, arr.ctypes.data
+        return cls._create(config, weights, dtype, False, ptr_of)
+
+    @classmethod
+    def from_device(cls, config, weights, dtype=F32) -> "DitBlock":
+        def ptr_of(t):
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError("device weights must be contiguous device tensors")
+            return t, t.data_ptr()
+        return cls._create(config, weights, dtype, True, ptr_of)
+
+    def set_runtime_shape(self, frames, height, width):
+        check(load().sv2_block_set_runtime_shape(self._h, frames, height, width),
+              "sv2_block_set_runtime_shape")
+        self.shape = (frames, height, width)
+
+    def workspace_size(self, text_len) -> int:
+        return check(load().sv2_block_workspace_size(self._h, text_len), "sv2_block_workspace_size")
+
+    def forward(self, vid, txt, emb, vid_out, txt_out, workspace=None, stream=None):
+        """vid [T*H*W, dim], txt [L, dim] (compute dtype), emb [6*dim] fp32."""
+        self._check_blobs(vid, txt, emb, vid_out, txt_out)
+        text_len = 0 if txt is None else txt.shape[0]
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(load().sv2_block_forward(self._h, _ptr(vid), _ptr(txt), text_len, _ptr(emb), _ptr(vid_out),
+                                       _ptr(txt_out), _ptr(workspace), ws_bytes, _stream(stream)),
+              "sv2_block_forward")
+
+    def set_debug(self, captures: dict | None):
+        """captures: {field: fp32 contiguous device tensor} for fields of
+        BLOCK_DEBUG_FIELDS, or None to stop capturing."""
+        if captures is None:
+            self._debug = None
+            check(load().sv2_block_set_debug(self._h, None), "sv2_block_set_debug")
+            return
+        d = BlockDebug()
+        for k, t in captures.items():
+            if k not in BLOCK_DEBUG_FIELDS:
+                raise KeyError(k)
+            if not (t.is_cuda and t.is_contiguous()) or t.dtype.itemsize != 4 or not t.dtype.is_floating_point:
+                raise ValueError(f"{k}: captures are contiguous fp32 device tensors")
+            setattr(d, k, t.data_ptr())
+        self._debug = captures
+        check(load().sv2_block_set_debug(self._h, ctypes.byref(d)), "sv2_block_set_debug")
+
+    def _check_blobs(self, vid, txt, emb, vid_out, txt_out):
+        """The blob checks of SeedVR2DiTBlock::forward (seedvr2_dit_block.cpp:
+        1119-1138) plus what the C ABI cannot see through plain pointers:
+        device, dtype and contiguity of every tensor."""
+        import torch
+        dim = self.config.dim
+        want = torch.float32 if self.dtype == F32 else torch.float16
+        shape = getattr(self, "shape", None)
+
+        def ok(t, rows):
+            return (t is not None and t.is_cuda and t.is_contiguous() and t.dtype == want and t.dim() == 2
+                    and t.shape[1] == dim and (rows is None or t.shape[0] == rows))
+
+        if shape is not None and not ok(vid, shape[0] * shape[1] * shape[2]):
+            raise ValueError(f"vid must be a contiguous {want} device tensor [T*H*W={shape}, {dim}]")
+        if shape is not None and not ok(vid_out, vid.shape[0]):
+            raise ValueError("vid_out must match vid")
+        if txt is not None and (not ok(txt, None) or not ok(txt_out, txt.shape[0])):
+            raise ValueError(f"txt / txt_out must be contiguous {want} device tensors [L, {dim}]")
+        if not (emb.is_cuda and emb.dtype == torch.float32 and emb.is_contiguous() and emb.numel() == 6 * dim):
+            raise ValueError(f"emb must be a contiguous fp32 device tensor of {6 * dim} values")
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            load().sv2_block_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -356,3 +356,28 @@ def _compose_explicit(orc, wts, vid, txt, emb, T, H, W, shared, last, shifted, D
                         heads=heads)
     finally:
         orc.window_attention = orig
+
+
+@pytest.mark.parametrize("last", [False, True])
+def test_block_stages_compose_to_forward(orc, last):
+    """head -> attention -> tail of the oracle equals its block forward bit for
+    bit, and the tail's pre-gate projections are proj_out(att) + bias."""
+    rng = np.random.default_rng(77 + last)
+    D, heads, F = 256, 2, 384
+    T, H, W, Lt = 2, 4, 6, 5
+    wts = {"vid": _rand_branch(rng, D, F), "txt": _rand_branch(rng, D, F), "freqs": reference_freqs()}
+    vid = rng.standard_normal((T * H * W, D)).astype(np.float32)
+    txt = rng.standard_normal((Lt, D)).astype(np.float32)
+    emb = rng.standard_normal(6 * D).astype(np.float32)
+    blk = orc.Block(wts, dim=D, heads=heads, mlp_hidden=F, last_layer=last, shifted=True)
+    qv, qt = blk.head(vid, txt, emb)
+    av, at = blk.attention(qv, qt, T, H, W)
+    vo, to, pv, pt = blk.tail(av, at, vid, txt, emb)
+    fv, ft = blk.forward(vid, txt, emb, T, H, W)
+    assert np.array_equal(vo, fv) and np.array_equal(to, ft)
+    want_pv = av.astype(np.float64) @ wts["vid"]["w_proj"].astype(np.float64).T + wts["vid"]["b_proj"]
+    assert np.abs(pv - want_pv).max() < 1e-4
+    if last:
+        # the last layer's text output is twice (proj + residual)
+        want_pt = at.astype(np.float64) @ wts["txt"]["w_proj"].astype(np.float64).T + wts["txt"]["b_proj"]
+        assert np.abs(to - 2 * (want_pt + txt)).max() < 1e-4
