@@ -35,8 +35,8 @@ WIN = (2, 9, 16)
 
 
 def plan_stats(shifted: bool):
-    import oracle
-    wins = oracle.make_windows(T, H, W, shifted, *WIN)
+    import sv2hip
+    wins = sv2hip.window_plan(sv2hip.rule(T, H, W, shifted, *WIN))
     sizes = [(w[1] - w[0]) * (w[3] - w[2]) * (w[5] - w[4]) for w in wins]
     flops = sum(4.0 * (v + L_TXT) ** 2 * HD * HEADS for v in sizes)
     return wins, sizes, flops
@@ -95,12 +95,115 @@ def cpu_baseline(target_s: float = 15.0):
     }
 
 
+DIT_DIM, DIT_FFN, DIT_BLOCKS, LATENT_C, TEXT_C, OUT_C = 2560, 6912, 32, 33, 5120, 16
+
+
+def dit_flops():
+    """Algorithmic flops of one DiT forward at 720p x 21f: every InnerProduct
+    (2 * rows * in * out) plus the windowed attention of the 16 unshifted and
+    16 shifted blocks (sum_w 4 * S_w^2 * 128 * 20)."""
+    Lv, D, F = T * H * W, DIT_DIM, DIT_FFN
+    gemm_block = 2.0 * (Lv + L_TXT) * D * (3 * D + D + 3 * F)
+    heads = 2.0 * Lv * 4 * LATENT_C * D + 2.0 * L_TXT * TEXT_C * D + 2.0 * Lv * D * 4 * OUT_C
+    attn = (DIT_BLOCKS // 2) * (plan_stats(False)[2] + plan_stats(True)[2])
+    return DIT_BLOCKS * gemm_block + heads, attn
+
+
+def dit_bench(dev, steps: int, warmup: int):
+    """The full 32-block DiT forward of one Euler step at 1280x720x21: latent
+    [33, 6, 90, 160] (16 noise + 16 condition channels N(0, 1), one channel of
+    ones), 58 text tokens of width 5120 N(0, 1), timestep 1000; fp16 weights
+    N(0, 0.02^2) generated on the device (q/k norm weights U(0.5, 1.5)),
+    resident in HBM; blocks alternate unshifted / shifted 2x9x16 windows as
+    the exporter lays them out (shared weights from block 10, the last block
+    with the last-layer text rule)."""
+    import torch
+    import sv2hip
+    from ncnn_files import MATRICES, block_flags, shapes
+    from parity import reference_freqs
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    D = DIT_DIM
+
+    def randn(shape, dtype, std=0.02):
+        return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std).to(dtype).contiguous()
+
+    wbytes = [0]
+
+    def branch():
+        out = {}
+        for f, shp in shapes(D, DIT_FFN).items():
+            if f in ("norm_q", "norm_k"):
+                out[f] = (torch.rand(shp, generator=g, device=dev) + 0.5).contiguous()
+            else:
+                out[f] = randn(shp, torch.float16 if f in MATRICES else torch.float32)
+            wbytes[0] += out[f].numel() * out[f].element_size()
+        return out
+
+    blocks = []
+    for i in range(DIT_BLOCKS):
+        shared, last, shifted = block_flags(i, DIT_BLOCKS)
+        w = {"vid": branch(), "freqs": reference_freqs()}
+        if not shared:
+            w["txt"] = branch()
+        cfg = sv2hip.block_config(block_index=i, shared_weights=int(shared), last_layer=int(last),
+                                  shifted_window=int(shifted), window_t=WIN[0], window_h=WIN[1], window_w=WIN[2])
+        blocks.append(sv2hip.DitBlock.from_device(cfg, w, sv2hip.F16))
+    f16, f32 = torch.float16, torch.float32
+    wi = {"w_vid": randn((D, 4 * LATENT_C), f16), "b_vid": randn((D,), f32),
+          "w_txt": randn((D, TEXT_C), f16), "b_txt": randn((D,), f32),
+          "w_time_in": randn((D, 256), f32), "b_time_in": randn((D,), f32),
+          "w_time_hid": randn((D, D), f32), "b_time_hid": randn((D,), f32),
+          "w_time_out": randn((6 * D, D), f32), "b_time_out": randn((6 * D,), f32)}
+    wo = {"norm_weight": (torch.rand((D,), generator=g, device=dev) + 0.5).contiguous(),
+          "shift": randn((D,), f32), "scale": randn((D,), f32),
+          "w_proj": randn((4 * OUT_C, D), f16), "b_proj": randn((4 * OUT_C,), f32)}
+    inp = sv2hip.DitInput.create(wi, sv2hip.F16, on_device=True)
+    outp = sv2hip.DitOutput.create(wo, sv2hip.F16, on_device=True)
+    dit = sv2hip.Dit.create(inp, blocks, outp)
+    latent = torch.randn((LATENT_C, T, 2 * H, 2 * W), generator=g, device=dev)
+    latent[LATENT_C - 1].fill_(1.0)
+    text = torch.randn((L_TXT, TEXT_C), generator=g, device=dev)
+    out = torch.empty((OUT_C, T, 2 * H, 2 * W), device=dev)
+    ws = torch.empty(dit.workspace_size(T, 2 * H, 2 * W, L_TXT), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        a.record(stream)
+        dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    finite = bool(torch.isfinite(out).all().item())
+    gemm_f, attn_f = dit_flops()
+    dit.close()
+    return {
+        "ms": round(ms, 3),
+        "steps": steps,
+        "tflop": round((gemm_f + attn_f) / 1e12, 2),
+        "tflops": round((gemm_f + attn_f) / (ms * 1e-3) / 1e12, 1),
+        "mfma_util": round((gemm_f + attn_f) / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+        "gemm_tflop": round(gemm_f / 1e12, 2),
+        "attention_tflop": round(attn_f / 1e12, 2),
+        "block_weights_gb": round(wbytes[0] / 1e9, 2),
+        "output_finite": finite,
+        "workload": ("SeedVR2-3B DiT forward, 1280x720x21 (latent 33x6x90x160 -> grid 6x45x80), 32 blocks, "
+                     "hidden 2560, 20 heads, MLP 6912 SwiGLU, 58 text tokens, windows 2x9x16 alternating "
+                     "unshifted / shifted, fp16 weights and activations, fp32 accumulation"),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--dit-steps", type=int, default=3, help="timed DiT forwards (0 skips the DiT leg)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a device buffer of BYTES three times (a plain copy kernel of known "
                          "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -206,6 +309,7 @@ def main():
             "mfma_util": round(tflops / PEAK_FP16_TFLOPS, 4),
             "variants": variants,
             "dit_step_ms": None,
+            "dit_step": None,
         },
         "roofline": {
             "bound": "hbm",
@@ -216,6 +320,10 @@ def main():
             "traffic": traffic,
         },
     }
+    if args.dit_steps > 0:
+        ds = dit_bench(dev, args.dit_steps, 1)
+        result["config"]["dit_step_ms"] = ds["ms"]
+        result["config"]["dit_step"] = ds
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))

@@ -290,6 +290,124 @@ typedef struct sv2_block_debug {
  * struct is copied; the arrays must stay valid while captures are enabled. */
 int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug);
 
+/* ------------------------------------------------------------------------
+ * The DiT input and output heads and the 32-block DiT forward
+ * (SeedVR2DiTInput, seedvr2_dit_input.{h,cpp}; SeedVR2DiTOutput,
+ * seedvr2_dit_output.{h,cpp}; SeedVR2DiT::forward, src/model/dit.cpp:
+ * 281-383).  Same parameters, weight order and blob layouts; latent, text
+ * and the DiT output are fp32 device arrays, the hidden streams between the
+ * heads and the blocks are in the compute dtype.
+ * ------------------------------------------------------------------------ */
+
+typedef struct sv2_dit_input_config {
+    int dim;             /* param 0 (2560) */
+    int video_channels;  /* param 1 (33) */
+    int text_channels;   /* param 2 (5120) */
+    int sinusoidal_dim;  /* param 3 (256) */
+    int embedding_dim;   /* param 4 (15360 = 6 * dim) */
+} sv2_dit_input_config;
+
+/* Weights of the input head in the exporter's order
+ * (tools/export_seedvr2_dit_ncnn.py:259-276).  Matrices [out][in]; biases fp32. */
+typedef struct sv2_dit_input_weights {
+    const void* w_vid;      /* [dim][4 * video_channels] */
+    const void* b_vid;      /* [dim] */
+    const void* w_txt;      /* [dim][text_channels] */
+    const void* b_txt;      /* [dim] */
+    const void* w_time_in;  /* [dim][sinusoidal_dim] */
+    const void* b_time_in;  /* [dim] */
+    const void* w_time_hid; /* [dim][dim] */
+    const void* b_time_hid; /* [dim] */
+    const void* w_time_out; /* [embedding_dim][dim] */
+    const void* b_time_out; /* [embedding_dim] */
+} sv2_dit_input_weights;
+
+typedef struct sv2_dit_input sv2_dit_input;
+
+/* Loads the SeedVR2DiTInput layer of an exported .param/.bin pair
+ * (seedvr2_dit_input.cpp:207-227).  Returns SV2_EINVAL when the parameters
+ * fail load_param's check (odd sinusoidal_dim, embedding_dim != 6 * dim). */
+int sv2_dit_input_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_dit_input** out);
+/* Creates the head from host fp32 (weights_on_device 0, converted and owned)
+ * or borrowed device weights (1): w_vid, w_txt in the compute dtype, the time
+ * MLP matrices and every bias fp32. */
+int sv2_dit_input_create(const sv2_dit_input_config* config, const sv2_dit_input_weights* weights,
+                         int weights_on_device, int compute_dtype, sv2_dit_input** out);
+int sv2_dit_input_get_config(const sv2_dit_input* head, sv2_dit_input_config* config);
+/* Device workspace bytes of a forward on the grid T x H x W (before the 2x2
+ * patchify) with text_len text tokens. */
+int64_t sv2_dit_input_workspace_size(const sv2_dit_input* head, int frames, int height, int width, int text_len);
+/* SeedVR2DiTInput::forward (seedvr2_dit_input.cpp:311-403): video fp32
+ * [T*H*W, video_channels] token-major (channel_major 0) or [video_channels][T][H][W]
+ * (channel_major 1), text fp32 [text_len, text_channels], timestep (the raw
+ * value, 1000 at the first Euler step).  Writes vid_out [T*(H/2)*(W/2), dim]
+ * and txt_out [text_len, dim] in the compute dtype and emb fp32 [embedding_dim].
+ * H and W must be even (:328-330). */
+int sv2_dit_input_forward(sv2_dit_input* head, const float* video, int channel_major, const float* text,
+                          int text_len, float timestep, int frames, int height, int width, void* vid_out,
+                          void* txt_out, float* emb, void* workspace, size_t workspace_bytes, void* stream);
+void sv2_dit_input_destroy(sv2_dit_input* head);
+
+typedef struct sv2_dit_output_config {
+    int dim;             /* param 0 (2560) */
+    int output_channels; /* param 1 (16) */
+    float norm_eps;      /* param 2 (1e-5) */
+} sv2_dit_output_config;
+
+/* Weights of the output head in the exporter's order
+ * (tools/export_seedvr2_dit_ncnn.py:289-293). */
+typedef struct sv2_dit_output_weights {
+    const void* norm_weight; /* [dim] fp32 */
+    const void* shift;       /* [dim] fp32 */
+    const void* scale;       /* [dim] fp32 */
+    const void* w_proj;      /* [4 * output_channels][dim] */
+    const void* b_proj;      /* [4 * output_channels] fp32 */
+} sv2_dit_output_weights;
+
+typedef struct sv2_dit_output sv2_dit_output;
+
+/* Loads the SeedVR2DiTOutput layer (seedvr2_dit_output.cpp:256-273). */
+int sv2_dit_output_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_dit_output** out);
+int sv2_dit_output_create(const sv2_dit_output_config* config, const sv2_dit_output_weights* weights,
+                          int weights_on_device, int compute_dtype, sv2_dit_output** out);
+int sv2_dit_output_get_config(const sv2_dit_output* head, sv2_dit_output_config* config);
+/* Workspace bytes of a forward over the patched grid T x h x w. */
+int64_t sv2_dit_output_workspace_size(const sv2_dit_output* head, int frames, int height, int width);
+/* SeedVR2DiTOutput::forward (seedvr2_dit_output.cpp:349-428): vid [T*h*w, dim]
+ * in the compute dtype and emb fp32 [6 * dim] give output fp32 on the grid
+ * T x 2h x 2w: token-major [T*2h*2w, output_channels] (channel_major 0) or
+ * [output_channels][T][2h][2w] (channel_major 1). */
+int sv2_dit_output_forward(sv2_dit_output* head, const void* vid, const float* emb, int frames, int height,
+                           int width, float* output, int channel_major, void* workspace, size_t workspace_bytes,
+                           void* stream);
+void sv2_dit_output_destroy(sv2_dit_output* head);
+
+typedef struct sv2_dit sv2_dit;
+
+/* Loads a whole exported DiT from `model_dir` (SeedVR2DiT::load, dit.cpp:
+ * 120-174, resident mode): seedvr2_dit_input.ncnn.{param,bin},
+ * seedvr2_dit_block_NN.ncnn.{param,bin} for NN = 00..31 and
+ * seedvr2_dit_output.ncnn.{param,bin}.  Every block is uploaded once. */
+int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out);
+/* Assembles a DiT from existing heads and blocks (borrowed; they must outlive
+ * the DiT and share its compute dtype). */
+int sv2_dit_create(sv2_dit_input* input, sv2_block* const* blocks, int block_count, sv2_dit_output* output,
+                   sv2_dit** out);
+/* Host.  The heads' parameters and the block count of a DiT. */
+int sv2_dit_get_config(const sv2_dit* dit, sv2_dit_input_config* input, sv2_dit_output_config* output,
+                       int* block_count);
+/* Workspace bytes of a forward on the latent grid T x H x W (H, W even) with
+ * text_len text tokens; sets every block's runtime shape to (T, H/2, W/2). */
+int64_t sv2_dit_workspace_size(sv2_dit* dit, int frames, int height, int width, int text_len);
+/* One DiT forward (SeedVR2DiT::forward, dit.cpp:281-383): latent fp32
+ * [video_channels][T][H][W], text fp32 [text_len, text_channels], the raw
+ * timestep; output fp32 [output_channels][T][H][W].  The input head, every
+ * block and the output head are enqueued on `stream` with no host
+ * synchronisation between them; the hidden streams stay in device memory. */
+int sv2_dit_forward(sv2_dit* dit, const float* latent, const float* text, int text_len, float timestep, int frames,
+                    int height, int width, float* output, void* workspace, size_t workspace_bytes, void* stream);
+void sv2_dit_destroy(sv2_dit* dit);
+
 /* Message of the last failure on the calling thread (never NULL). */
 const char* sv2_last_error(void);
 

@@ -66,6 +66,19 @@ class OrcBlock(ctypes.Structure):
     ]
 
 
+class OrcDitInput(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("dim", "video_channels", "text_channels", "sinusoidal_dim",
+                                            "embedding_dim")] + \
+               [(n, ctypes.c_void_p) for n in ("w_vid", "b_vid", "w_txt", "b_txt", "w_tin", "b_tin", "w_thid",
+                                               "b_thid", "w_tout", "b_tout")] + [("threads", ctypes.c_int)]
+
+
+class OrcDitOutput(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_int), ("output_channels", ctypes.c_int), ("eps", ctypes.c_float)] + \
+               [(n, ctypes.c_void_p) for n in ("norm", "shift", "scale", "w_proj", "b_proj")] + \
+               [("threads", ctypes.c_int)]
+
+
 def load() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
@@ -96,6 +109,11 @@ def load() -> ctypes.CDLL:
     lib.orc_block_attention.restype = i
     lib.orc_block_tail.argtypes = [ctypes.POINTER(OrcBlock), vp, i, vp, i, vp, vp, vp, vp, vp, vp, vp]
     lib.orc_block_tail.restype = i
+    lib.orc_dit_input_forward.argtypes = [ctypes.POINTER(OrcDitInput), vp, vp, i, ctypes.c_float, i, i, i,
+                                          vp, vp, vp]
+    lib.orc_dit_input_forward.restype = i
+    lib.orc_dit_output_forward.argtypes = [ctypes.POINTER(OrcDitOutput), vp, vp, i, i, i, vp]
+    lib.orc_dit_output_forward.restype = i
     _lib = lib
     return lib
 
@@ -286,3 +304,58 @@ def block_forward(weights, vid, txt, emb, T, H, W, *, dim, heads, head_dim=128, 
                 last_layer=last_layer, shifted=shifted, wt=wt, wh=wh, ww=ww, rope_mode=rope_mode, theta=theta,
                 qk_norm=qk_norm, threads=threads)
     return blk.forward(vid, txt, emb, T, H, W)
+
+
+INPUT_FIELDS = ("w_vid", "b_vid", "w_txt", "b_txt", "w_time_in", "b_time_in", "w_time_hid", "b_time_hid",
+                "w_time_out", "b_time_out")
+OUTPUT_FIELDS = ("norm_weight", "shift", "scale", "w_proj", "b_proj")
+
+
+def dit_input_forward(weights, video, text, timestep, T, H, W, *, sinusoidal_dim=256, threads=0):
+    """The DiT input head.  weights: {field: array} of INPUT_FIELDS; video
+    [T*H*W, C] token-major fp32, text [L, text_channels].  Returns
+    (vid_out [T*(H/2)*(W/2), dim], txt_out [L, dim], emb [6*dim])."""
+    arrs = {k: _f32(weights[k]) for k in INPUT_FIELDS}
+    dim = arrs["b_vid"].shape[0]
+    video, text = _f32(video), _f32(text)
+    C, tc = video.shape[1], arrs["w_txt"].shape[1]
+    cfg = OrcDitInput(dim, C, tc, sinusoidal_dim, arrs["b_time_out"].shape[0],
+                      *[_p(arrs[k]) for k in INPUT_FIELDS], threads)
+    rows = T * (H // 2) * (W // 2)
+    vo = np.zeros((rows, dim), np.float32)
+    to = np.zeros((text.shape[0], dim), np.float32)
+    emb = np.zeros(arrs["b_time_out"].shape[0], np.float32)
+    rc = load().orc_dit_input_forward(ctypes.byref(cfg), _p(video), _p(text), text.shape[0], ctypes.c_float(timestep),
+                                      T, H, W, _p(vo), _p(to), _p(emb))
+    if rc != 0:
+        raise RuntimeError(f"orc_dit_input_forward failed: {rc}")
+    return vo, to, emb
+
+
+def dit_output_forward(weights, vid, emb, T, h, w, *, eps=1e-5, threads=0):
+    """The DiT output head.  weights: {field: array} of OUTPUT_FIELDS; vid
+    [T*h*w, dim].  Returns [T*2h*2w, output_channels] token-major."""
+    arrs = {k: _f32(weights[k]) for k in OUTPUT_FIELDS}
+    vid, emb = _f32(vid), _f32(emb)
+    dim = vid.shape[1]
+    oc = arrs["b_proj"].shape[0] // 4
+    cfg = OrcDitOutput(dim, oc, eps, *[_p(arrs[k]) for k in OUTPUT_FIELDS], threads)
+    out = np.zeros((T * 4 * h * w, oc), np.float32)
+    rc = load().orc_dit_output_forward(ctypes.byref(cfg), _p(vid), _p(emb), T, h, w, _p(out))
+    if rc != 0:
+        raise RuntimeError(f"orc_dit_output_forward failed: {rc}")
+    return out
+
+
+def dit_forward(input_weights, blocks, output_weights, latent, text, timestep, *, eps=1e-5, threads=0):
+    """SeedVR2DiT::forward (dit.cpp:281-383) composed from the oracle's heads
+    and blocks.  latent [C, T, H, W] fp32 (channel-major, as the engine holds
+    it), blocks: Block objects in order.  Returns [16, T, H, W]."""
+    C, T, H, W = latent.shape
+    flat = np.ascontiguousarray(np.transpose(latent, (1, 2, 3, 0)).reshape(T * H * W, C))  # dit.cpp:66-80
+    vid, txt, emb = dit_input_forward(input_weights, flat, text, timestep, T, H, W, threads=threads)
+    for blk in blocks:
+        vid, txt = blk.forward(vid, txt, emb, T, H // 2, W // 2)
+    out = dit_output_forward(output_weights, vid, emb, T, H // 2, W // 2, eps=eps, threads=threads)
+    oc = out.shape[1]
+    return np.ascontiguousarray(np.transpose(out.reshape(T, H, W, oc), (3, 0, 1, 2)))  # dit.cpp:82-95

@@ -673,3 +673,116 @@ done:
     free(att_t);
     return rc;
 }
+
+static float silu_f(float v)
+{
+    return v / (1.f + expf(-v));
+}
+
+/* seedvr2_dit_input.cpp:311-403 */
+int orc_dit_input_forward(const orc_dit_input* in, const float* video, const float* text, int L, float timestep,
+                          int T, int H, int W, float* vid_out, float* txt_out, float* emb)
+{
+    const int C = in->video_channels, D = in->dim, S = in->sinusoidal_dim;
+    if (T <= 0 || H <= 0 || W <= 0 || H % 2 != 0 || W % 2 != 0 || L < 0 || S % 2 != 0 ||
+        in->embedding_dim != 6 * D)
+        return -1;
+    const int h = H / 2, w = W / 2, rows = T * h * w;
+    float* patches = (float*)malloc(sizeof(float) * (size_t)rows * 4 * C);
+    float* sinus = (float*)malloc(sizeof(float) * (size_t)S);
+    float* h1 = (float*)malloc(sizeof(float) * (size_t)D);
+    float* h2 = (float*)malloc(sizeof(float) * (size_t)D);
+    if (!patches || !sinus || !h1 || !h2)
+    {
+        free(patches);
+        free(sinus);
+        free(h1);
+        free(h2);
+        return -100;
+    }
+    /* :336-352 patch p = (t, y, x) on the patched grid; its 4 source
+     * positions in (dy, dx) order, video_channels values each */
+    for (int p = 0; p < rows; p++)
+    {
+        const int x = p % w, y = (p / w) % h, t = p / (w * h);
+        float* dst = patches + (size_t)p * 4 * C;
+        for (int dy = 0; dy < 2; dy++)
+            for (int dx = 0; dx < 2; dx++)
+            {
+                const size_t src = ((size_t)(t * H + y * 2 + dy) * W + x * 2 + dx) * C;
+                memcpy(dst, video + src, sizeof(float) * C);
+                dst += C;
+            }
+    }
+    orc_inner_product(patches, rows, 4 * C, in->w_vid, in->b_vid, D, vid_out, in->threads);
+    orc_inner_product(text, L, in->text_channels, in->w_txt, in->b_txt, D, txt_out, in->threads);
+    /* :360-392 */
+    const int half = S / 2;
+    for (int i = 0; i < half; i++)
+    {
+        const float frequency = expf(-logf(10000.f) * (float)i / (float)half);
+        const float value = timestep * frequency;
+        sinus[i] = sinf(value);
+        sinus[i + half] = cosf(value);
+    }
+    orc_inner_product(sinus, 1, S, in->w_tin, in->b_tin, D, h1, in->threads);
+    for (int i = 0; i < D; i++)
+        h1[i] = silu_f(h1[i]);
+    orc_inner_product(h1, 1, D, in->w_thid, in->b_thid, D, h2, in->threads);
+    for (int i = 0; i < D; i++)
+        h2[i] = silu_f(h2[i]);
+    orc_inner_product(h2, 1, D, in->w_tout, in->b_tout, in->embedding_dim, emb, in->threads);
+    free(patches);
+    free(sinus);
+    free(h1);
+    free(h2);
+    return 0;
+}
+
+/* seedvr2_dit_output.cpp:349-428 */
+int orc_dit_output_forward(const orc_dit_output* o, const float* vid, const float* emb, int T, int h, int w,
+                           float* out)
+{
+    const int D = o->dim, OC = o->output_channels, rows = T * h * w;
+    if (T <= 0 || h <= 0 || w <= 0 || D <= 0 || OC <= 0)
+        return -1;
+    float* normed = (float*)calloc((size_t)rows * D, sizeof(float));
+    float* proj = (float*)malloc(sizeof(float) * (size_t)rows * 4 * OC);
+    if (!normed || !proj)
+    {
+        free(normed);
+        free(proj);
+        return -100;
+    }
+    for (int r = 0; r < rows; r++)
+    {
+        const float* x = vid + (size_t)r * D;
+        float* y = normed + (size_t)r * D;
+        double ss = 0.0;
+        for (int c = 0; c < D; c++)
+            ss += (double)x[c] * x[c];
+        const float inv = 1.f / sqrtf((float)(ss / D) + o->eps);
+        for (int c = 0; c < D; c++)
+        {
+            const float value = x[c] * inv * o->norm[c];
+            y[c] = value * (emb[c * 6 + 1] + o->scale[c]) + emb[c * 6] + o->shift[c];
+        }
+    }
+    orc_inner_product(normed, rows, D, o->w_proj, o->b_proj, 4 * OC, proj, o->threads);
+    const int H = 2 * h, W = 2 * w;
+    for (int p = 0; p < rows; p++)
+    {
+        const int x = p % w, y = (p / w) % h, t = p / (w * h);
+        const float* src = proj + (size_t)p * 4 * OC;
+        for (int dy = 0; dy < 2; dy++)
+            for (int dx = 0; dx < 2; dx++)
+            {
+                float* dst = out + ((size_t)(t * H + y * 2 + dy) * W + x * 2 + dx) * OC;
+                memcpy(dst, src, sizeof(float) * OC);
+                src += OC;
+            }
+    }
+    free(normed);
+    free(proj);
+    return 0;
+}

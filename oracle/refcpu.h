@@ -30,6 +30,11 @@
  *   orc_block_forward   composition of the above; parity unpinned against
  *                       the reference block itself (no stored golden outputs
  *                       exist in the reference and ncnn is absent)
+ *   orc_dit_input_forward, orc_dit_output_forward
+ *                       patchify / unpatchify against an einops-style numpy
+ *                       reshape, the sinusoid and time MLP against a float64
+ *                       numpy evaluation, timestep 0 special case, identity
+ *                       projections that expose the permutations exactly
  */
 #ifndef SEEDVR2_REFCPU_H
 #define SEEDVR2_REFCPU_H
@@ -159,6 +164,33 @@ int orc_block_tail(const orc_block* blk, const float* att_v, int Lv, const float
                    const float* txt, const float* emb, float* vid_out, float* txt_out, float* proj_v, float* proj_t);
 int orc_block_forward(const orc_block* blk, const float* vid, int Lv, const float* txt, int Lt,
                       const float* emb, int T, int H, int W, float* vid_out, float* txt_out);
+
+/* The DiT input head (seedvr2_dit_input.cpp:311-403).  Matrices [out][in]. */
+typedef struct orc_dit_input {
+    int dim, video_channels, text_channels, sinusoidal_dim, embedding_dim;
+    const float *w_vid, *b_vid, *w_txt, *b_txt;
+    const float *w_tin, *b_tin, *w_thid, *b_thid, *w_tout, *b_tout;
+    int threads;
+} orc_dit_input;
+
+/* video [T*H*W, video_channels] token-major, text [L, text_channels];
+ * writes vid_out [T*(H/2)*(W/2), dim], txt_out [L, dim], emb [embedding_dim].
+ * Returns -1 for an odd H or W or a bad config (:317-330). */
+int orc_dit_input_forward(const orc_dit_input* in, const float* video, const float* text, int L, float timestep,
+                          int T, int H, int W, float* vid_out, float* txt_out, float* emb);
+
+/* The DiT output head (seedvr2_dit_output.cpp:349-428). */
+typedef struct orc_dit_output {
+    int dim, output_channels;
+    float eps;
+    const float *norm, *shift, *scale, *w_proj, *b_proj;
+    int threads;
+} orc_dit_output;
+
+/* vid [T*h*w, dim], emb [6*dim]; writes out [T*2h*2w, output_channels]
+ * token-major. */
+int orc_dit_output_forward(const orc_dit_output* o, const float* vid, const float* emb, int T, int h, int w,
+                           float* out);
 
 #ifdef __cplusplus
 }

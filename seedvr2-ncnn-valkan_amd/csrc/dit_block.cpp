@@ -3,17 +3,15 @@
 // .param/.bin pair, and the block forward as a chain of the library's kernels
 // on one stream — token RMSNorm + ada, the QKV / proj / MLP InnerProducts as
 // rocBLAS GEMMs, the windowed attention, gated residuals and SwiGLU.
-#include <rocblas/rocblas.h>
-
 #include <algorithm>
 #include <cstring>
-#include <map>
-#include <mutex>
 #include <string>
 #include <vector>
 
 #include "ncnn_format.h"
 #include "sv2_internal.h"
+
+using sv2::gemm_rows;
 
 namespace
 {
@@ -34,52 +32,6 @@ struct DevBranch
 size_t dtype_size(int dtype)
 {
     return dtype == SV2_F32 ? 4 : 2;
-}
-
-// One rocBLAS handle per device, shared by every block of the process.
-rocblas_handle blas_handle(int* rc)
-{
-    static std::mutex mutex;
-    static std::map<int, rocblas_handle> handles;
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess)
-    {
-        *rc = sv2::hip_error(err, "block: hipGetDevice");
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lock(mutex);
-    auto it = handles.find(device);
-    if (it != handles.end())
-        return it->second;
-    rocblas_handle h = nullptr;
-    if (rocblas_create_handle(&h) != rocblas_status_success)
-    {
-        *rc = sv2::set_error(SV2_EDEVICE, "block: rocblas_create_handle failed");
-        return nullptr;
-    }
-    handles[device] = h;
-    return h;
-}
-
-// y[rows, out] = x[rows, in] W^T with W [out][in] row-major (the InnerProduct
-// of the reference without its bias), fp32 accumulation.
-int gemm_rows(rocblas_handle h, hipStream_t stream, int dtype, int rows, int in, int out, const void* x,
-              const void* w, void* y)
-{
-    if (rows == 0)
-        return SV2_OK;
-    const rocblas_datatype t = dtype == SV2_F32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
-    const float alpha = 1.f;
-    const float beta = 0.f;
-    rocblas_set_stream(h, stream);
-    // column-major view: Y^T [out x rows] = W [out x in] * X^T [in x rows]
-    const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, out, rows, in,
-                                              &alpha, w, t, in, x, t, in, &beta, y, t, out, y, t, out,
-                                              rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return sv2::set_error(SV2_EDEVICE, std::string("block: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
-    return SV2_OK;
 }
 
 } // namespace
@@ -108,11 +60,11 @@ struct sv2_block
     ~sv2_block()
     {
         for (void* p : owned)
-            hipFree(p);
+            (void)hipFree(p);
         if (rope)
-            hipFree(rope);
+            (void)hipFree(rope);
         if (ws)
-            hipFree(ws);
+            (void)hipFree(ws);
     }
 };
 
@@ -138,27 +90,7 @@ int validate_config(const sv2_block_config& c)
 // or kept fp32 (vectors, dtype SV2_F32).
 int upload(sv2_block* b, const float* host, size_t count, int dtype, const void** dev)
 {
-    void* p = nullptr;
-    const size_t bytes = count * dtype_size(dtype);
-    hipError_t err = hipMalloc(&p, bytes ? bytes : 4);
-    if (err != hipSuccess)
-        return sv2::hip_error(err, "block: hipMalloc of weights");
-    b->owned.push_back(p);
-    if (dtype == SV2_F32)
-    {
-        err = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
-    }
-    else
-    {
-        std::vector<_Float16> half(count);
-        for (size_t i = 0; i < count; i++)
-            half[i] = static_cast<_Float16>(host[i]);
-        err = hipMemcpy(p, half.data(), bytes, hipMemcpyHostToDevice);
-    }
-    if (err != hipSuccess)
-        return sv2::hip_error(err, "block: hipMemcpy of weights");
-    *dev = p;
-    return SV2_OK;
+    return sv2::upload_weights(&b->owned, host, count, dtype, dev);
 }
 
 int bind_branch(sv2_block* b, const sv2_block_branch& in, bool on_device, DevBranch* out)
@@ -247,7 +179,7 @@ int ensure_rope(sv2_block* b, int text_len, hipStream_t stream)
         hipError_t err = hipStreamSynchronize(stream);
         if (err != hipSuccess)
             return sv2::hip_error(err, "block: synchronize before RoPE table resize");
-        hipFree(b->rope);
+        (void)hipFree(b->rope);
         b->rope = nullptr;
     }
     if (!b->rope)
@@ -354,7 +286,7 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
 // The MLP of one branch on rows [rows, D]: RMSNorm + ada (mlp shift/scale),
 // gate and in InnerProducts, SwiGLU, out InnerProduct, gated residual with x
 // (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).
-int branch_mlp(const sv2_block* b, rocblas_handle h, hipStream_t stream, const DevBranch& br, const float* emb,
+int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, const float* emb,
                const void* x, int rows, void* out, char* m, char* g, char* u)
 {
     if (rows == 0)
@@ -363,17 +295,47 @@ int branch_mlp(const sv2_block* b, rocblas_handle h, hipStream_t stream, const D
     int rc;
     if ((rc = sv2_rmsnorm_ada(x, m, dt, rows, D, b->cfg.norm_eps, emb, br.ada[3], br.ada[4], 3, 1, stream)) != SV2_OK)
         return rc;
-    if ((rc = gemm_rows(h, stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
-        (rc = gemm_rows(h, stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
+    if ((rc = gemm_rows(stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
+        (rc = gemm_rows(stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
         return rc;
     if ((rc = sv2_swiglu(g, u, dt, static_cast<int64_t>(rows) * F, stream)) != SV2_OK)
         return rc;
-    if ((rc = gemm_rows(h, stream, dt, rows, F, D, g, br.w_out, out)) != SV2_OK)
+    if ((rc = gemm_rows(stream, dt, rows, F, D, g, br.w_out, out)) != SV2_OK)
         return rc;
     return sv2_ada_residual(out, x, dt, rows, D, emb, br.ada[5], 3, 0, stream);
 }
 
 } // namespace
+
+int sv2::upload_weights(std::vector<void*>* owned, const float* host, size_t count, int dtype, const void** dev)
+{
+    void* p = nullptr;
+    const size_t bytes = count * (dtype == SV2_F32 ? 4 : 2);
+    hipError_t err = hipMalloc(&p, bytes ? bytes : 4);
+    if (err != hipSuccess)
+        return sv2::hip_error(err, "hipMalloc of weights");
+    owned->push_back(p);
+    if (dtype == SV2_F32)
+    {
+        err = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
+    }
+    else
+    {
+        std::vector<_Float16> half(count);
+        for (size_t i = 0; i < count; i++)
+            half[i] = static_cast<_Float16>(host[i]);
+        err = hipMemcpy(p, half.data(), bytes, hipMemcpyHostToDevice);
+    }
+    if (err != hipSuccess)
+        return sv2::hip_error(err, "hipMemcpy of weights");
+    *dev = p;
+    return SV2_OK;
+}
+
+int sv2::block_compute_dtype(const sv2_block* block)
+{
+    return block->dtype;
+}
 
 extern "C" {
 
@@ -571,7 +533,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                 hipError_t err = hipStreamSynchronize(stream); // queued work may still use the old buffer
                 if (err != hipSuccess)
                     return hip_error(err, "sv2_block_forward: synchronize before workspace resize");
-                hipFree(b->ws);
+                (void)hipFree(b->ws);
                 b->ws = nullptr;
                 b->ws_bytes = 0;
             }
@@ -586,9 +548,6 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
         ws = static_cast<char*>(b->ws);
     }
     if ((rc = ensure_rope(b, text_len, stream)) != SV2_OK)
-        return rc;
-    rocblas_handle h = blas_handle(&rc);
-    if (!h)
         return rc;
 
     const sv2_block_config& c = b->cfg;
@@ -610,7 +569,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
     if ((rc = sv2_rmsnorm_ada(vid, xa, dt, Lv, D, c.norm_eps, emb, vb.ada[0], vb.ada[1], 0, 1, stream)) != SV2_OK)
         return rc;
-    if ((rc = gemm_rows(h, stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
+    if ((rc = gemm_rows(stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
         return rc;
     const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
     auto capture = [&](float* dst, const void* src, int rows, int cols) {
@@ -623,7 +582,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
         if ((rc = sv2_rmsnorm_ada(txt, xa, dt, Lt, D, c.norm_eps, emb, tb.ada[0], tb.ada[1], 0, c.last_layer ? 0 : 1,
                                   stream)) != SV2_OK)
             return rc;
-        if ((rc = gemm_rows(h, stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
+        if ((rc = gemm_rows(stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
             return rc;
         if (dbg && (rc = capture(dbg->qkv_txt, qkv_t, Lt, 3 * D)) != SV2_OK)
             return rc;
@@ -642,7 +601,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                 (Lt > 0 && (rc = capture(dbg->attention_txt, att_t, Lt, D)) != SV2_OK)))
         return rc;
     // output projections with bias, gated residuals (:1180-1209)
-    if ((rc = gemm_rows(h, stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK ||
+    if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK ||
         (rc = launch_bias_rows(p_v, vb.b_proj, dt, Lv, D, stream)) != SV2_OK)
         return rc;
     if (dbg && (rc = capture(dbg->projected_vid, p_v, Lv, D)) != SV2_OK)
@@ -651,7 +610,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
         return rc;
     if (Lt > 0)
     {
-        if ((rc = gemm_rows(h, stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK ||
+        if ((rc = gemm_rows(stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK ||
             (rc = launch_bias_rows(p_t, tb.b_proj, dt, Lt, D, stream)) != SV2_OK)
             return rc;
         if (dbg && (rc = capture(dbg->projected_txt, p_t, Lt, D)) != SV2_OK)
@@ -662,7 +621,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
             return rc;
     }
     // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)
-    if ((rc = branch_mlp(b, h, stream, vb, emb, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
+    if ((rc = branch_mlp(b, stream, vb, emb, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
         return rc;
     if (Lt > 0)
     {
@@ -675,7 +634,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
             if ((rc = sv2_ada_residual(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 0, 2, stream)) != SV2_OK)
                 return rc;
         }
-        else if ((rc = branch_mlp(b, h, stream, tb, emb, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
+        else if ((rc = branch_mlp(b, stream, tb, emb, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
         {
             return rc;
         }

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "seedvr2_hip.h"
 
@@ -115,6 +116,26 @@ int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int 
 int launch_rmsnorm_ada(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* emb,
                        const float* shift, const float* scale, const float* gamma, int slot_base, int has_ada,
                        hipStream_t stream);
+
+// y[rows, out] = x[rows, in] W^T, W [out][in] row-major (an InnerProduct
+// without its bias), in dtype (SV2_F32 or SV2_F16) with fp32 accumulation,
+// on rocBLAS; enqueued on `stream`.
+int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y);
+
+// Allocates device memory for `count` host fp32 values, stores them as dtype
+// (SV2_F32 or SV2_F16, round to nearest) and records the allocation in *owned.
+int upload_weights(std::vector<void*>* owned, const float* host, size_t count, int dtype, const void** dev);
+
+// The compute dtype a block was created with.
+int block_compute_dtype(const sv2_block* block);
+
+// Head kernels (dit_heads.hip).
+int launch_patchify(const float* video, void* patches, int dtype, int T, int h, int w, int C, int channel_major,
+                    hipStream_t stream);
+int launch_unpatchify(const void* projected, float* output, int dtype, int T, int h, int w, int OC, int channel_major,
+                      hipStream_t stream);
+int launch_sinusoid(float* out, float timestep, int dim, hipStream_t stream);
+int launch_from_f32(void* dst, const float* src, int dtype, long long count, hipStream_t stream);
 
 // dst (fp32) = src (dtype); count a multiple of 8.
 int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipStream_t stream);

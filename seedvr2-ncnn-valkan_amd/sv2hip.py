@@ -45,6 +45,24 @@ EXPORTS = [
     "sv2_block_forward",
     "sv2_block_destroy",
     "sv2_block_set_debug",
+    "sv2_dit_input_load",
+    "sv2_dit_input_create",
+    "sv2_dit_input_get_config",
+    "sv2_dit_input_workspace_size",
+    "sv2_dit_input_forward",
+    "sv2_dit_input_destroy",
+    "sv2_dit_output_load",
+    "sv2_dit_output_create",
+    "sv2_dit_output_get_config",
+    "sv2_dit_output_workspace_size",
+    "sv2_dit_output_forward",
+    "sv2_dit_output_destroy",
+    "sv2_dit_load",
+    "sv2_dit_create",
+    "sv2_dit_get_config",
+    "sv2_dit_workspace_size",
+    "sv2_dit_forward",
+    "sv2_dit_destroy",
     "sv2_last_error",
     "sv2_version",
 ]
@@ -139,6 +157,30 @@ class BlockDebug(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in BLOCK_DEBUG_FIELDS]
 
 
+class DitInputConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("dim", "video_channels", "text_channels", "sinusoidal_dim",
+                                            "embedding_dim")]
+
+
+INPUT_FIELDS = ("w_vid", "b_vid", "w_txt", "b_txt", "w_time_in", "b_time_in", "w_time_hid", "b_time_hid",
+                "w_time_out", "b_time_out")
+
+
+class DitInputWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in INPUT_FIELDS]
+
+
+class DitOutputConfig(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_int), ("output_channels", ctypes.c_int), ("norm_eps", ctypes.c_float)]
+
+
+OUTPUT_FIELDS = ("norm_weight", "shift", "scale", "w_proj", "b_proj")
+
+
+class DitOutputWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in OUTPUT_FIELDS]
+
+
 _lib = None
 
 
@@ -195,6 +237,46 @@ def load() -> ctypes.CDLL:
     lib.sv2_block_set_debug.restype = i
     lib.sv2_block_destroy.argtypes = [vp]
     lib.sv2_block_destroy.restype = None
+    c_f = ctypes.c_float
+    lib.sv2_dit_input_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i, ctypes.POINTER(vp)]
+    lib.sv2_dit_input_load.restype = i
+    lib.sv2_dit_input_create.argtypes = [ctypes.POINTER(DitInputConfig), ctypes.POINTER(DitInputWeights), i, i,
+                                         ctypes.POINTER(vp)]
+    lib.sv2_dit_input_create.restype = i
+    lib.sv2_dit_input_get_config.argtypes = [vp, ctypes.POINTER(DitInputConfig)]
+    lib.sv2_dit_input_get_config.restype = i
+    lib.sv2_dit_input_workspace_size.argtypes = [vp, i, i, i, i]
+    lib.sv2_dit_input_workspace_size.restype = ctypes.c_int64
+    lib.sv2_dit_input_forward.argtypes = [vp, vp, i, vp, i, c_f, i, i, i, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.sv2_dit_input_forward.restype = i
+    lib.sv2_dit_input_destroy.argtypes = [vp]
+    lib.sv2_dit_input_destroy.restype = None
+    lib.sv2_dit_output_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i, ctypes.POINTER(vp)]
+    lib.sv2_dit_output_load.restype = i
+    lib.sv2_dit_output_create.argtypes = [ctypes.POINTER(DitOutputConfig), ctypes.POINTER(DitOutputWeights), i, i,
+                                          ctypes.POINTER(vp)]
+    lib.sv2_dit_output_create.restype = i
+    lib.sv2_dit_output_get_config.argtypes = [vp, ctypes.POINTER(DitOutputConfig)]
+    lib.sv2_dit_output_get_config.restype = i
+    lib.sv2_dit_output_workspace_size.argtypes = [vp, i, i, i]
+    lib.sv2_dit_output_workspace_size.restype = ctypes.c_int64
+    lib.sv2_dit_output_forward.argtypes = [vp, vp, vp, i, i, i, vp, i, vp, ctypes.c_size_t, vp]
+    lib.sv2_dit_output_forward.restype = i
+    lib.sv2_dit_output_destroy.argtypes = [vp]
+    lib.sv2_dit_output_destroy.restype = None
+    lib.sv2_dit_load.argtypes = [ctypes.c_char_p, i, ctypes.POINTER(vp)]
+    lib.sv2_dit_load.restype = i
+    lib.sv2_dit_create.argtypes = [vp, ctypes.POINTER(vp), i, vp, ctypes.POINTER(vp)]
+    lib.sv2_dit_create.restype = i
+    lib.sv2_dit_get_config.argtypes = [vp, ctypes.POINTER(DitInputConfig), ctypes.POINTER(DitOutputConfig),
+                                       ctypes.POINTER(i)]
+    lib.sv2_dit_get_config.restype = i
+    lib.sv2_dit_workspace_size.argtypes = [vp, i, i, i, i]
+    lib.sv2_dit_workspace_size.restype = ctypes.c_int64
+    lib.sv2_dit_forward.argtypes = [vp, vp, vp, i, c_f, i, i, i, vp, vp, ctypes.c_size_t, vp]
+    lib.sv2_dit_forward.restype = i
+    lib.sv2_dit_destroy.argtypes = [vp]
+    lib.sv2_dit_destroy.restype = None
     lib.sv2_last_error.argtypes = []
     lib.sv2_last_error.restype = ctypes.c_char_p
     lib.sv2_version.argtypes = []
@@ -504,3 +586,194 @@ class DitBlock:
             self.close()
         except Exception:
             pass
+
+
+def _host_f32(a):
+    arr = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    return arr, arr.ctypes.data
+
+
+def _dev_ptr(t):
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("device weights must be contiguous device tensors")
+    return t, t.data_ptr()
+
+
+def _need_f32_dev(t, numel, what):
+    import torch
+    if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float32 and t.numel() == numel):
+        raise ValueError(f"{what} must be a contiguous fp32 device tensor of {numel} values")
+
+
+class _Handle:
+    _destroy = None
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            getattr(load(), self._destroy)(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DitInput(_Handle):
+    """The SeedVR2DiTInput head (sv2_dit_input_*)."""
+    _destroy = "sv2_dit_input_destroy"
+
+    def __init__(self, handle, dtype, keep=None):
+        self._h = ctypes.c_void_p(handle)
+        self.dtype = dtype
+        self._keep = keep
+        self.config = DitInputConfig()
+        check(load().sv2_dit_input_get_config(self._h, ctypes.byref(self.config)), "sv2_dit_input_get_config")
+
+    @classmethod
+    def load(cls, param_path, bin_path, dtype=F32):
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_input_load(str(param_path).encode(), str(bin_path).encode(), dtype, ctypes.byref(h)),
+              "sv2_dit_input_load")
+        return cls(h.value, dtype)
+
+    @classmethod
+    def create(cls, weights, dtype=F32, *, on_device=False, video_channels=None, sinusoidal_dim=None):
+        keep, ptrs = [], {}
+        for k in INPUT_FIELDS:
+            arr, p = (_dev_ptr if on_device else _host_f32)(weights[k])
+            keep.append(arr)
+            ptrs[k] = p
+        dim = int(weights["b_vid"].shape[0])
+        cfg = DitInputConfig(dim, video_channels or int(weights["w_vid"].shape[1]) // 4,
+                             int(weights["w_txt"].shape[1]), sinusoidal_dim or int(weights["w_time_in"].shape[1]),
+                             int(weights["b_time_out"].shape[0]))
+        w = DitInputWeights(*[ptrs[k] for k in INPUT_FIELDS])
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_input_create(ctypes.byref(cfg), ctypes.byref(w), int(on_device), dtype, ctypes.byref(h)),
+              "sv2_dit_input_create")
+        return cls(h.value, dtype, keep if on_device else None)
+
+    def forward(self, video, text, timestep, T, H, W, vid_out, txt_out, emb, *, channel_major=False,
+                workspace=None, stream=None):
+        """video fp32 [T*H*W, C] (or [C, T, H, W] with channel_major), text fp32
+        [L, text_channels]; vid_out / txt_out in the compute dtype, emb fp32."""
+        import torch
+        c = self.config
+        want = torch.float32 if self.dtype == F32 else torch.float16
+        _need_f32_dev(video, T * H * W * c.video_channels, "video")
+        L = 0 if text is None else text.shape[0]
+        if L:
+            _need_f32_dev(text, L * c.text_channels, "text")
+            if not (txt_out.is_cuda and txt_out.is_contiguous() and txt_out.dtype == want
+                    and txt_out.numel() == L * c.dim):
+                raise ValueError("txt_out shape/dtype")
+        if not (vid_out.is_cuda and vid_out.is_contiguous() and vid_out.dtype == want
+                and vid_out.numel() == T * (H // 2) * (W // 2) * c.dim):
+            raise ValueError("vid_out shape/dtype")
+        _need_f32_dev(emb, c.embedding_dim, "emb")
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(load().sv2_dit_input_forward(self._h, _ptr(video), int(channel_major), _ptr(text), L,
+                                           ctypes.c_float(timestep), T, H, W, _ptr(vid_out), _ptr(txt_out if L else None),
+                                           _ptr(emb), _ptr(workspace), ws_bytes, _stream(stream)),
+              "sv2_dit_input_forward")
+
+
+class DitOutput(_Handle):
+    """The SeedVR2DiTOutput head (sv2_dit_output_*)."""
+    _destroy = "sv2_dit_output_destroy"
+
+    def __init__(self, handle, dtype, keep=None):
+        self._h = ctypes.c_void_p(handle)
+        self.dtype = dtype
+        self._keep = keep
+        self.config = DitOutputConfig()
+        check(load().sv2_dit_output_get_config(self._h, ctypes.byref(self.config)), "sv2_dit_output_get_config")
+
+    @classmethod
+    def load(cls, param_path, bin_path, dtype=F32):
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_output_load(str(param_path).encode(), str(bin_path).encode(), dtype, ctypes.byref(h)),
+              "sv2_dit_output_load")
+        return cls(h.value, dtype)
+
+    @classmethod
+    def create(cls, weights, dtype=F32, *, on_device=False, eps=1e-5):
+        keep, ptrs = [], {}
+        for k in OUTPUT_FIELDS:
+            arr, p = (_dev_ptr if on_device else _host_f32)(weights[k])
+            keep.append(arr)
+            ptrs[k] = p
+        cfg = DitOutputConfig(int(weights["norm_weight"].shape[0]), int(weights["b_proj"].shape[0]) // 4, eps)
+        w = DitOutputWeights(*[ptrs[k] for k in OUTPUT_FIELDS])
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_output_create(ctypes.byref(cfg), ctypes.byref(w), int(on_device), dtype,
+                                           ctypes.byref(h)), "sv2_dit_output_create")
+        return cls(h.value, dtype, keep if on_device else None)
+
+    def forward(self, vid, emb, T, h, w, output, *, channel_major=False, workspace=None, stream=None):
+        import torch
+        c = self.config
+        want = torch.float32 if self.dtype == F32 else torch.float16
+        if not (vid.is_cuda and vid.is_contiguous() and vid.dtype == want and vid.numel() == T * h * w * c.dim):
+            raise ValueError("vid shape/dtype")
+        _need_f32_dev(emb, 6 * c.dim, "emb")
+        _need_f32_dev(output, T * 4 * h * w * c.output_channels, "output")
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(load().sv2_dit_output_forward(self._h, _ptr(vid), _ptr(emb), T, h, w, _ptr(output), int(channel_major),
+                                            _ptr(workspace), ws_bytes, _stream(stream)), "sv2_dit_output_forward")
+
+
+class Dit(_Handle):
+    """The whole DiT (sv2_dit_*): input head, blocks, output head."""
+    _destroy = "sv2_dit_destroy"
+
+    def __init__(self, handle, dtype, parts=None):
+        self._h = ctypes.c_void_p(handle)
+        self.dtype = dtype
+        self._parts = parts  # borrowed heads and blocks kept alive
+        ic, oc, n = DitInputConfig(), DitOutputConfig(), ctypes.c_int()
+        check(load().sv2_dit_get_config(self._h, ctypes.byref(ic), ctypes.byref(oc), ctypes.byref(n)),
+              "sv2_dit_get_config")
+        self.input_config, self.output_config, self.block_count = ic, oc, n.value
+        self.video_channels = ic.video_channels
+        self.text_channels = ic.text_channels
+        self.output_channels = oc.output_channels
+
+    @classmethod
+    def load(cls, model_dir, dtype=F32):
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_load(str(model_dir).encode(), dtype, ctypes.byref(h)), "sv2_dit_load")
+        return cls(h.value, dtype)
+
+    @classmethod
+    def create(cls, input_head, blocks, output_head):
+        arr = (ctypes.c_void_p * max(len(blocks), 1))(*[b._h.value for b in blocks])
+        h = ctypes.c_void_p()
+        check(load().sv2_dit_create(input_head._h, arr, len(blocks), output_head._h, ctypes.byref(h)),
+              "sv2_dit_create")
+        return cls(h.value, input_head.dtype, (input_head, list(blocks), output_head))
+
+    def workspace_size(self, T, H, W, text_len) -> int:
+        return check(load().sv2_dit_workspace_size(self._h, T, H, W, text_len), "sv2_dit_workspace_size")
+
+    def forward(self, latent, text, timestep, output, *, workspace=None, stream=None):
+        """latent fp32 [C, T, H, W], text fp32 [L, text_channels], output fp32
+        [output_channels, T, H, W] (device tensors)."""
+        import torch
+        C, T, H, W = latent.shape
+        for name, t in (("latent", latent), ("output", output)):
+            if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float32):
+                raise ValueError(f"{name} must be a contiguous fp32 device tensor")
+        if tuple(output.shape[1:]) != (T, H, W):
+            raise ValueError("output must be [output_channels, T, H, W]")
+        if C != self.video_channels or output.shape[0] != self.output_channels:
+            raise ValueError("latent / output channel counts differ from the heads")
+        L = 0 if text is None else text.shape[0]
+        if L and not (text.is_cuda and text.is_contiguous() and text.dtype == torch.float32 and text.dim() == 2
+                      and text.shape[1] == self.text_channels):
+            raise ValueError("text must be a contiguous fp32 device tensor [L, text_channels]")
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(load().sv2_dit_forward(self._h, _ptr(latent), _ptr(text), L, ctypes.c_float(timestep), T, H, W,
+                                     _ptr(output), _ptr(workspace), ws_bytes, _stream(stream)), "sv2_dit_forward")

@@ -190,3 +190,97 @@ def runner_inputs(dim: int, T: int, H: int, W: int, text_len: int):
     txt = runner_fill(dim, text_len, 100)
     emb = runner_fill(dim * 6, 1, 200).reshape(-1)
     return vid, txt, emb
+
+
+# --- the DiT input / output heads and a whole model directory -------------
+
+INPUT_FIELDS = ("w_vid", "b_vid", "w_txt", "b_txt", "w_time_in", "b_time_in", "w_time_hid", "b_time_hid",
+                "w_time_out", "b_time_out")
+OUTPUT_FIELDS = ("norm_weight", "shift", "scale", "w_proj", "b_proj")
+
+
+def _write_layer_param(path: Path, layer_type: str, inputs, outputs, params: str) -> None:
+    lines = [f"Input input_{n} 0 1 {n}" for n in inputs]
+    lines.append(" ".join([layer_type, path.stem, str(len(inputs)), str(len(outputs)), *inputs, *outputs, params]))
+    path.write_text(f"7767517\n{len(lines)} {len(set(inputs) | set(outputs))}\n" + "\n".join(lines) + "\n")
+
+
+def write_input_files(param: Path, binf: Path, weights: dict, *, dim, video_channels=33, text_channels=5120,
+                      sinusoidal_dim=256, storage="fp16") -> dict:
+    """tools/export_seedvr2_dit_ncnn.py:251-279: each InnerProduct writes its
+    tagged matrix, then its raw bias.  Returns the decoded weights."""
+    _write_layer_param(param, "SeedVR2DiTInput", ("vid", "txt", "timestep", "vid_shape"),
+                       ("vid_out", "txt_out", "emb", "patched_shape"),
+                       f"0={dim} 1={video_channels} 2={text_channels} 3={sinusoidal_dim} 4={6 * dim}")
+    dec = {}
+    with open(binf, "wb") as out:
+        for f in INPUT_FIELDS:
+            a = np.ascontiguousarray(weights[f], dtype=np.float32)
+            if f.startswith("w_"):
+                dec[f] = _tagged(out, a, storage).reshape(a.shape)
+            else:
+                out.write(a.astype("<f4").tobytes())
+                dec[f] = a
+    return dec
+
+
+def write_output_files(param: Path, binf: Path, weights: dict, *, dim, output_channels=16, eps="1e-05",
+                       storage="fp16") -> dict:
+    """tools/export_seedvr2_dit_ncnn.py:282-297: norm weight, out shift, out
+    scale (raw), the tagged projection matrix, its raw bias."""
+    _write_layer_param(param, "SeedVR2DiTOutput", ("vid", "emb", "vid_shape"), ("vid_out", "output_shape"),
+                       f"0={dim} 1={output_channels} 2={eps}")
+    dec = {}
+    with open(binf, "wb") as out:
+        for f in OUTPUT_FIELDS:
+            a = np.ascontiguousarray(weights[f], dtype=np.float32)
+            if f == "w_proj":
+                dec[f] = _tagged(out, a, storage).reshape(a.shape)
+            else:
+                out.write(a.astype("<f4").tobytes())
+                dec[f] = a
+    return dec
+
+
+def random_input_weights(rng, dim, *, video_channels=33, text_channels=5120, sinusoidal_dim=256, std=0.02):
+    shp = {"w_vid": (dim, 4 * video_channels), "b_vid": (dim,), "w_txt": (dim, text_channels), "b_txt": (dim,),
+           "w_time_in": (dim, sinusoidal_dim), "b_time_in": (dim,), "w_time_hid": (dim, dim),
+           "b_time_hid": (dim,), "w_time_out": (6 * dim, dim), "b_time_out": (6 * dim,)}
+    return {k: (rng.standard_normal(s, dtype=np.float32) * np.float32(std)).astype(np.float16).astype(np.float32)
+            for k, s in shp.items()}
+
+
+def random_output_weights(rng, dim, *, output_channels=16, std=0.02):
+    w = {"norm_weight": rng.uniform(0.5, 1.5, dim).astype(np.float32),
+         "shift": rng.standard_normal(dim, dtype=np.float32) * np.float32(std),
+         "scale": rng.standard_normal(dim, dtype=np.float32) * np.float32(std),
+         "w_proj": rng.standard_normal((4 * output_channels, dim), dtype=np.float32) * np.float32(std),
+         "b_proj": rng.standard_normal(4 * output_channels, dtype=np.float32) * np.float32(std)}
+    return {k: v.astype(np.float16).astype(np.float32) for k, v in w.items()}
+
+
+def block_flags(index: int, count: int = 32):
+    """The exporter's per-block flags (tools/export_seedvr2_dit_ncnn.py:204-206):
+    shared weights from block 10, last layer, odd blocks shifted."""
+    return index >= 10, index == count - 1, index % 2 == 1
+
+
+def write_model_dir(root: Path, input_w, blocks_w, output_w, *, dim, heads, mlp_hidden, video_channels=33,
+                    text_channels=5120, output_channels=16, storage="fp16") -> dict:
+    """A whole DiT directory in the layout SeedVR2DiT::load reads
+    (src/model/dit.cpp:120-174).  Returns the decoded weights."""
+    root.mkdir(parents=True, exist_ok=True)
+    dec = {"input": write_input_files(root / "seedvr2_dit_input.ncnn.param", root / "seedvr2_dit_input.ncnn.bin",
+                                      input_w, dim=dim, video_channels=video_channels,
+                                      text_channels=text_channels, storage=storage),
+           "output": write_output_files(root / "seedvr2_dit_output.ncnn.param",
+                                        root / "seedvr2_dit_output.ncnn.bin", output_w, dim=dim,
+                                        output_channels=output_channels, storage=storage),
+           "blocks": []}
+    for i, w in enumerate(blocks_w):
+        shared, last, shifted = block_flags(i, len(blocks_w))
+        stem = f"seedvr2_dit_block_{i:02d}.ncnn"
+        write_param(root / f"{stem}.param", index=i, shared=shared, last=last, shifted=shifted, dim=dim,
+                    heads=heads, mlp_hidden=mlp_hidden)
+        dec["blocks"].append(write_bin(root / f"{stem}.bin", w, shared=shared, storage=storage))
+    return dec

@@ -159,3 +159,62 @@ def test_runner_fills():
     assert w["vid"]["w_qkv"].shape == (384, 128)
     assert w["vid"]["w_proj"][0, 0] == np.float32(0.005) * np.float32(7 % 7 - 3)
     assert w["vid"]["b_proj"][1] == np.float32(0.01) * np.float32((1 + 7) % 5 - 2)
+
+
+# --- the DiT heads and the model directory loader -------------------------
+
+def _head_load(hip, fn, param, binf):
+    h = ctypes.c_void_p()
+    rc = getattr(hip.load(), fn)(str(param).encode(), str(binf).encode(), hip.F32, ctypes.byref(h))
+    assert not h.value
+    return rc, hip.load().sv2_last_error().decode()
+
+
+def _head_files(tmp_path, which, **kw):
+    rng = np.random.default_rng(2)
+    param, binf = tmp_path / f"{which}.param", tmp_path / f"{which}.bin"
+    if which == "input":
+        w = nf.random_input_weights(rng, 16, video_channels=2, text_channels=8, sinusoidal_dim=8)
+        nf.write_input_files(param, binf, w, dim=16, video_channels=2, text_channels=8, sinusoidal_dim=8, **kw)
+    else:
+        w = nf.random_output_weights(rng, 16, output_channels=2)
+        nf.write_output_files(param, binf, w, dim=16, output_channels=2, **kw)
+    return param, binf
+
+
+def test_input_head_param_checks(hip, tmp_path):
+    param, binf = _head_files(tmp_path, "input")
+    # load_param rejects embedding_dim != 6 * dim (seedvr2_dit_input.cpp:214)
+    param.write_text(param.read_text().replace("4=96", "4=95"))
+    rc, msg = _head_load(hip, "sv2_dit_input_load", param, binf)
+    assert rc == hip.SV2_EINVAL and "embedding_dim" in msg
+    param.write_text(param.read_text().replace("4=95", "4=96").replace("3=8", "3=7"))
+    rc, _ = _head_load(hip, "sv2_dit_input_load", param, binf)
+    assert rc == hip.SV2_EINVAL
+
+
+def test_input_head_truncated(hip, tmp_path):
+    param, binf = _head_files(tmp_path, "input")
+    binf.write_bytes(binf.read_bytes()[:-4])
+    rc, msg = _head_load(hip, "sv2_dit_input_load", param, binf)
+    assert rc == hip.SV2_EDEVICE and "ended early" in msg
+
+
+def test_output_head_checks(hip, tmp_path):
+    param, binf = _head_files(tmp_path, "output")
+    binf.write_bytes(binf.read_bytes()[:-1])
+    rc, msg = _head_load(hip, "sv2_dit_output_load", param, binf)
+    assert rc == hip.SV2_EDEVICE and "ended early" in msg
+    param.write_text(param.read_text().replace("SeedVR2DiTOutput", "SeedVR2DiTInput"))
+    rc, msg = _head_load(hip, "sv2_dit_output_load", param, binf)
+    assert rc == hip.SV2_EINVAL
+
+
+def test_model_dir_missing_file(hip, tmp_path):
+    """SeedVR2DiT::load checks all 34 file pairs before loading any
+    (src/model/dit.cpp:122-134)."""
+    _head_files(tmp_path, "input")
+    h = ctypes.c_void_p()
+    rc = hip.load().sv2_dit_load(str(tmp_path).encode(), hip.F32, ctypes.byref(h))
+    assert rc == hip.SV2_EINVAL and not h.value
+    assert "seedvr2_dit_input.ncnn.param" in hip.load().sv2_last_error().decode()

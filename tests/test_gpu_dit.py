@@ -1,0 +1,248 @@
+"""GPU parity of the DiT heads and the 32-block DiT forward against the
+oracle (SeedVR2DiTInput, seedvr2_dit_input.cpp:311-403; SeedVR2DiTOutput,
+seedvr2_dit_output.cpp:349-428; SeedVR2DiT::forward, src/model/dit.cpp:
+281-383).
+
+Gates:
+  * heads in fp32 compute mode: max-abs <= 2e-3 and mean-abs <= 2e-4 after
+    fp32 upcast; in fp16 mode NRMSE <= 2e-3;
+  * the whole DiT (32 blocks): the reference's full-model criteria, NRMSE <=
+    0.02 and cosine >= 0.9998 (tools/test_seedvr2_dit_ncnn.py:249-250), in
+    both compute modes, with max/mean-abs reported.
+The heads run at the real widths (dim 2560, 33 latent channels, 5120 text
+channels, 256 sinusoid, 16 output channels) on a small grid; the DiT runs at
+width 256 (2 heads, MLP 512) with the exporter's 32-block layout (shared
+weights from block 10, last layer 31, odd blocks shifted) so the oracle
+finishes in seconds.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import ncnn_files as nf
+
+pytestmark = pytest.mark.gpu
+
+
+def metrics(gpu, ref) -> dict:
+    g = np.asarray(gpu, np.float64)
+    r = np.asarray(ref, np.float64)
+    assert g.shape == r.shape, (g.shape, r.shape)
+    d = g - r
+    rms = max(float(np.sqrt(np.mean(r * r))), 1e-12)
+    den = max(float(np.sqrt(np.sum(g * g) * np.sum(r * r))), 1e-12)
+    return {"finite": bool(np.isfinite(g).all()), "max_abs": float(np.abs(d).max()),
+            "mean_abs": float(np.abs(d).mean()), "nrmse": float(np.sqrt(np.mean(d * d))) / rms,
+            "cosine": float(np.sum(g * r) / den)}
+
+
+def gate_head(rep, strict, what):
+    print(f"[{what}] {rep}", flush=True)
+    assert rep["finite"], what
+    if strict:
+        assert rep["max_abs"] <= 2e-3 and rep["mean_abs"] <= 2e-4, f"{what}: {rep}"
+    else:
+        assert rep["nrmse"] <= 2e-3, f"{what}: {rep}"
+
+
+def gate_full(rep, what):
+    print(f"[{what}] {rep}", flush=True)
+    assert rep["finite"] and rep["nrmse"] <= 0.02 and rep["cosine"] >= 0.9998, f"{what}: {rep}"
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device="cuda:0", dtype=dtype)
+
+
+def cdt(hip, code):
+    return torch.float32 if code == hip.F32 else torch.float16
+
+
+def run_input(hip, head, video, text, t, T, H, W, *, channel_major=False):
+    c = head.config
+    td = cdt(hip, head.dtype)
+    rows = T * (H // 2) * (W // 2)
+    vo = torch.full((rows, c.dim), float("nan"), device="cuda:0", dtype=td)
+    to = torch.full((text.shape[0], c.dim), float("nan"), device="cuda:0", dtype=td)
+    emb = torch.full((c.embedding_dim,), float("nan"), device="cuda:0")
+    head.forward(dev(video), dev(text), t, T, H, W, vo, to, emb, channel_major=channel_major)
+    torch.cuda.synchronize()
+    return vo.float().cpu().numpy(), to.float().cpu().numpy(), emb.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_input_head(hip, orc, device, dtype):
+    code = hip.F32 if dtype == "f32" else hip.F16
+    print(f"[input head] {dtype}", flush=True)
+    rng = np.random.default_rng(41)
+    dim, T, H, W, L = 2560, 2, 8, 12, 58
+    w = nf.random_input_weights(rng, dim)
+    video = rng.standard_normal((T * H * W, 33), dtype=np.float32)
+    text = rng.standard_normal((L, 5120), dtype=np.float32)
+    if code == hip.F16:
+        text = text.astype(np.float16).astype(np.float32)
+    head = hip.DitInput.create(w, code)
+    try:
+        gv, gt, ge = run_input(hip, head, video, text, 1000.0, T, H, W)
+        # the channel-major latent gives the same result
+        cm = np.ascontiguousarray(video.reshape(T, H, W, 33).transpose(3, 0, 1, 2))
+        gv2, _, _ = run_input(hip, head, cm, text, 1000.0, T, H, W, channel_major=True)
+        assert np.array_equal(gv, gv2)
+    finally:
+        head.close()
+    rv, rt, re = orc.dit_input_forward(w, video, text, 1000.0, T, H, W)
+    strict = code == hip.F32
+    gate_head(metrics(gv, rv), strict, f"input vid {dtype}")
+    gate_head(metrics(gt, rt), strict, f"input txt {dtype}")
+    # emb is computed in fp32 in both modes; the device's sinf/cosf of
+    # timestep * f_i (arguments up to 1000) may differ from the host's by an ulp
+    gate_head(metrics(ge, re), True, f"input emb {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_output_head(hip, orc, device, dtype):
+    code = hip.F32 if dtype == "f32" else hip.F16
+    print(f"[output head] {dtype}", flush=True)
+    rng = np.random.default_rng(42)
+    dim, T, h, w = 2560, 2, 4, 6
+    wts = nf.random_output_weights(rng, dim)
+    vid = rng.standard_normal((T * h * w, dim), dtype=np.float32) * 3
+    if code == hip.F16:
+        vid = vid.astype(np.float16).astype(np.float32)
+    emb = rng.standard_normal(6 * dim, dtype=np.float32)
+    head = hip.DitOutput.create(wts, code)
+    try:
+        out = torch.full((T * 4 * h * w, 16), float("nan"), device="cuda:0")
+        head.forward(dev(vid, cdt(hip, code)), dev(emb), T, h, w, out)
+        out_cm = torch.full((16, T, 2 * h, 2 * w), float("nan"), device="cuda:0")
+        head.forward(dev(vid, cdt(hip, code)), dev(emb), T, h, w, out_cm, channel_major=True)
+        torch.cuda.synchronize()
+        g = out.cpu().numpy()
+        assert np.array_equal(g.reshape(T, 2 * h, 2 * w, 16).transpose(3, 0, 1, 2), out_cm.cpu().numpy())
+    finally:
+        head.close()
+    r = orc.dit_output_forward(wts, vid, emb, T, h, w)
+    gate_head(metrics(g, r), code == hip.F32, f"output {dtype}")
+
+
+def test_heads_loader(hip, orc, device, tmp_path):
+    """Heads loaded from exported files give the same outputs as heads
+    created from the decoded weights."""
+    rng = np.random.default_rng(43)
+    dim = 256
+    wi = nf.random_input_weights(rng, dim, text_channels=64)
+    wo = nf.random_output_weights(rng, dim)
+    di = nf.write_input_files(tmp_path / "i.param", tmp_path / "i.bin", wi, dim=dim, text_channels=64)
+    do = nf.write_output_files(tmp_path / "o.param", tmp_path / "o.bin", wo, dim=dim)
+    T, H, W, L = 1, 4, 6, 5
+    video = rng.standard_normal((T * H * W, 33), dtype=np.float32)
+    text = rng.standard_normal((L, 64), dtype=np.float32)
+    a = hip.DitInput.load(tmp_path / "i.param", tmp_path / "i.bin")
+    b = hip.DitInput.create(di)
+    oa = hip.DitOutput.load(tmp_path / "o.param", tmp_path / "o.bin")
+    ob = hip.DitOutput.create(do)
+    try:
+        assert (a.config.dim, a.config.video_channels, a.config.text_channels, a.config.sinusoidal_dim,
+                a.config.embedding_dim) == (dim, 33, 64, 256, 6 * dim)
+        ra, rb = run_input(hip, a, video, text, 500.0, T, H, W), run_input(hip, b, video, text, 500.0, T, H, W)
+        for x, y in zip(ra, rb):
+            assert np.array_equal(x, y)
+        outs = []
+        for head in (oa, ob):
+            out = torch.empty((T * H * W, 16), device="cuda:0")
+            head.forward(dev(ra[0]), dev(ra[2]), T, H // 2, W // 2, out)
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+        assert np.array_equal(outs[0], outs[1])
+    finally:
+        for x in (a, b, oa, ob):
+            x.close()
+
+
+SMALL = dict(dim=256, heads=2, mlp_hidden=512, text_channels=64)
+
+
+def small_dit_weights(seed, n_blocks=32):
+    rng = np.random.default_rng(seed)
+    D, F = SMALL["dim"], SMALL["mlp_hidden"]
+    wi = nf.random_input_weights(rng, D, text_channels=SMALL["text_channels"])
+    wo = nf.random_output_weights(rng, D)
+    blocks = [nf.random_weights(rng, D, F, shared=nf.block_flags(i, n_blocks)[0]) for i in range(n_blocks)]
+    return wi, blocks, wo
+
+
+def build_dit(hip, wi, blocks_w, wo, code):
+    D = SMALL["dim"]
+    inp = hip.DitInput.create(wi, code)
+    out = hip.DitOutput.create(wo, code)
+    blocks = []
+    for i, w in enumerate(blocks_w):
+        shared, last, shifted = nf.block_flags(i, len(blocks_w))
+        cfg = hip.block_config(block_index=i, shared_weights=int(shared), last_layer=int(last),
+                               shifted_window=int(shifted), dim=D, heads=SMALL["heads"],
+                               mlp_hidden=SMALL["mlp_hidden"])
+        blocks.append(hip.DitBlock.from_host(cfg, w, code))
+    return hip.Dit.create(inp, blocks, out)
+
+
+def oracle_dit(orc, wi, blocks_w, wo, latent, text, t):
+    oblocks = []
+    for i, w in enumerate(blocks_w):
+        shared, last, shifted = nf.block_flags(i, len(blocks_w))
+        oblocks.append(orc.Block(w, dim=SMALL["dim"], heads=SMALL["heads"], mlp_hidden=SMALL["mlp_hidden"],
+                                 shared=shared, last_layer=last, shifted=shifted))
+    return orc.dit_forward(wi, oblocks, wo, latent, text, t)
+
+
+def run_dit(hip, dit, latent, text, t, *, workspace=False):
+    C, T, H, W = latent.shape
+    out = torch.full((16, T, H, W), float("nan"), device="cuda:0")
+    ws = None
+    if workspace:
+        ws = torch.empty(dit.workspace_size(T, H, W, text.shape[0]), dtype=torch.uint8, device="cuda:0")
+    dit.forward(dev(latent), dev(text), t, out, workspace=ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_dit_32_blocks(hip, orc, device, dtype):
+    code = hip.F32 if dtype == "f32" else hip.F16
+    print(f"[dit 32 blocks] {dtype}", flush=True)
+    wi, blocks_w, wo = small_dit_weights(44)
+    rng = np.random.default_rng(45)
+    T, H, W, L = 2, 8, 12, 9
+    latent = rng.standard_normal((33, T, H, W), dtype=np.float32)
+    text = rng.standard_normal((L, SMALL["text_channels"]), dtype=np.float32)
+    dit = build_dit(hip, wi, blocks_w, wo, code)
+    try:
+        g = run_dit(hip, dit, latent, text, 1000.0)
+        g2 = run_dit(hip, dit, latent, text, 1000.0, workspace=True)
+        assert np.array_equal(g, g2)
+    finally:
+        dit.close()
+    r = oracle_dit(orc, wi, blocks_w, wo, latent, text, 1000.0)
+    gate_full(metrics(g, r), f"dit {dtype}")
+
+
+def test_dit_load_model_dir(hip, orc, device, tmp_path):
+    """sv2_dit_load of an exported 34-file directory equals the DiT assembled
+    from the same decoded weights."""
+    wi, blocks_w, wo = small_dit_weights(46)
+    dec = nf.write_model_dir(tmp_path / "dit", wi, blocks_w, wo, dim=SMALL["dim"], heads=SMALL["heads"],
+                             mlp_hidden=SMALL["mlp_hidden"], text_channels=SMALL["text_channels"])
+    rng = np.random.default_rng(47)
+    latent = rng.standard_normal((33, 1, 6, 8), dtype=np.float32)
+    text = rng.standard_normal((4, SMALL["text_channels"]), dtype=np.float32)
+    loaded = hip.Dit.load(tmp_path / "dit", hip.F16)
+    assert loaded.block_count == 32 and loaded.text_channels == SMALL["text_channels"]
+    built = build_dit(hip, dec["input"], dec["blocks"], dec["output"], hip.F16)
+    try:
+        a = run_dit(hip, loaded, latent, text, 750.0)
+        b = run_dit(hip, built, latent, text, 750.0)
+        assert np.array_equal(a, b)
+    finally:
+        loaded.close()
+        built.close()
