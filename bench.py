@@ -204,6 +204,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--dit-steps", type=int, default=3, help="timed DiT forwards (0 skips the DiT leg)")
+    ap.add_argument("--dit-only", action="store_true",
+                    help="run only the DiT leg and print its figures (for profiling the DiT step)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a device buffer of BYTES three times (a plain copy kernel of known "
                          "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -226,6 +228,9 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
         return
     sv2hip.load()
+    if args.dit_only:
+        print(json.dumps({"dit_step": dit_bench(dev, max(args.dit_steps, 1), 1)}))
+        return
     D = HEADS * HD
     rng = np.random.default_rng(0)
     vid = torch.from_numpy(rng.standard_normal((T * H * W, 3 * D), dtype=np.float32)).to(dev, torch.float16)

@@ -175,7 +175,7 @@ InputWs input_layout(const sv2_dit_input* in, int T, int H, int W, int L)
 
 struct OutputWs
 {
-    size_t normed, projected, total;
+    size_t table, normed, projected, total;
 };
 
 OutputWs output_layout(const sv2_dit_output* out, int T, int h, int w)
@@ -184,6 +184,8 @@ OutputWs output_layout(const sv2_dit_output* out, int T, int h, int w)
     const size_t Lp = static_cast<size_t>(T) * h * w;
     OutputWs o{};
     size_t off = 0;
+    o.table = off;
+    off = align256(off + 3 * static_cast<size_t>(out->cfg.dim) * sizeof(float));
     o.normed = off;
     off = align256(off + Lp * out->cfg.dim * es);
     o.projected = off;
@@ -556,8 +558,10 @@ int sv2_dit_output_forward(sv2_dit_output* o, const void* vid, const float* emb,
     void* projected = ws + lay.projected;
     // RMSNorm * norm_weight + ada with emb slot 0 (:368-386), vid_out.proj
     // with bias (:388-390), unpatchify (:391-413)
-    if ((rc = launch_rmsnorm_ada(vid, normed, dt, Lp, c.dim, c.norm_eps, emb, o->shift, o->scale, o->norm, 0, 1,
-                                 stream)) != SV2_OK ||
+    float* table = reinterpret_cast<float*>(ws + lay.table);
+    if ((rc = launch_ada_table(emb, o->scale, nullptr, 0, c.dim, table, stream)) != SV2_OK ||
+        (rc = launch_rmsnorm_table(vid, normed, dt, Lp, c.dim, c.norm_eps, table, o->shift, o->norm, 1, stream)) !=
+            SV2_OK ||
         (rc = gemm_rows(stream, dt, Lp, c.dim, P, normed, o->w_proj, projected)) != SV2_OK ||
         (rc = launch_bias_rows(projected, o->b_proj, dt, Lp, P, stream)) != SV2_OK ||
         (rc = launch_unpatchify(projected, output, dt, frames, height, width, c.output_channels, channel_major,

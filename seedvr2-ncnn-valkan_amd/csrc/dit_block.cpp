@@ -228,7 +228,7 @@ sv2_attn_args attention_args(const sv2_block* b, int text_len)
 // p_v [Lv, D], p_t [Lt, D], g and u [R, F], attention workspace; R = max(Lv, Lt).
 struct BlockWorkspace
 {
-    size_t xa, qkv_v, qkv_t, att_v, att_t, p_v, p_t, g, u, attn, total;
+    size_t tables, xa, qkv_v, qkv_t, att_v, att_t, p_v, p_t, g, u, attn, total;
 };
 
 size_t align256(size_t v)
@@ -259,6 +259,8 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
     if (attn < 0)
         return static_cast<int>(attn);
     size_t off = 0;
+    w->tables = off; // four ada tables [3][D] fp32: video attention, video MLP, text attention, text MLP
+    off = align256(off + 12 * D * sizeof(float));
     w->xa = off;
     off = align256(off + R * D * es);
     w->qkv_v = off;
@@ -285,15 +287,18 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
 
 // The MLP of one branch on rows [rows, D]: RMSNorm + ada (mlp shift/scale),
 // gate and in InnerProducts, SwiGLU, out InnerProduct, gated residual with x
-// (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).
-int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, const float* emb,
-               const void* x, int rows, void* out, char* m, char* g, char* u)
+// (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).  `table` is the
+// branch's MLP modulation table.
+int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, const float* table, const void* x,
+               int rows, void* out, char* m, char* g, char* u)
 {
+    using namespace sv2;
     if (rows == 0)
         return SV2_OK;
     const int D = b->cfg.dim, F = b->cfg.mlp_hidden, dt = b->dtype;
     int rc;
-    if ((rc = sv2_rmsnorm_ada(x, m, dt, rows, D, b->cfg.norm_eps, emb, br.ada[3], br.ada[4], 3, 1, stream)) != SV2_OK)
+    if ((rc = launch_rmsnorm_table(x, m, dt, rows, D, b->cfg.norm_eps, table, br.ada[3], nullptr, 1, stream)) !=
+        SV2_OK)
         return rc;
     if ((rc = gemm_rows(stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
         (rc = gemm_rows(stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
@@ -302,7 +307,7 @@ int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, cons
         return rc;
     if ((rc = gemm_rows(stream, dt, rows, F, D, g, br.w_out, out)) != SV2_OK)
         return rc;
-    return sv2_ada_residual(out, x, dt, rows, D, emb, br.ada[5], 3, 0, stream);
+    return launch_residual_table(out, x, dt, rows, D, table, nullptr, 0, stream);
 }
 
 } // namespace
@@ -566,8 +571,21 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     char* u = ws + w.u;
     const size_t es = dtype_size(dt);
 
+    // ada modulation tables of this layer: the emb blob's slots combined with
+    // the branch vectors once, read as contiguous rows by the kernels below
+    float* tables = reinterpret_cast<float*>(ws + w.tables);
+    float* tab_va = tables;
+    float* tab_vm = tables + 3 * D;
+    float* tab_ta = tables + 6 * D;
+    float* tab_tm = tables + 9 * D;
+    if ((rc = launch_ada_table(emb, vb.ada[1], vb.ada[2], 0, D, tab_va, stream)) != SV2_OK ||
+        (rc = launch_ada_table(emb, vb.ada[4], vb.ada[5], 3, D, tab_vm, stream)) != SV2_OK)
+        return rc;
+    if (Lt > 0 && ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
+                   (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
+        return rc;
     // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
-    if ((rc = sv2_rmsnorm_ada(vid, xa, dt, Lv, D, c.norm_eps, emb, vb.ada[0], vb.ada[1], 0, 1, stream)) != SV2_OK)
+    if ((rc = launch_rmsnorm_table(vid, xa, dt, Lv, D, c.norm_eps, tab_va, vb.ada[0], nullptr, 1, stream)) != SV2_OK)
         return rc;
     if ((rc = gemm_rows(stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
         return rc;
@@ -575,12 +593,19 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     auto capture = [&](float* dst, const void* src, int rows, int cols) {
         return dst ? launch_to_f32(dst, src, dt, static_cast<long long>(rows) * cols, stream) : SV2_OK;
     };
+    // the projection before the gate: proj_out + bias, in fp32
+    auto capture_projected = [&](float* dst, const void* src, const float* bias, int rows) {
+        if (!dst)
+            return SV2_OK;
+        const int r = launch_to_f32(dst, src, dt, static_cast<long long>(rows) * D, stream);
+        return r != SV2_OK ? r : launch_bias_rows(dst, bias, SV2_F32, rows, D, stream);
+    };
     if (dbg && (rc = capture(dbg->qkv_vid, qkv_v, Lv, 3 * D)) != SV2_OK)
         return rc;
     if (Lt > 0)
     {
-        if ((rc = sv2_rmsnorm_ada(txt, xa, dt, Lt, D, c.norm_eps, emb, tb.ada[0], tb.ada[1], 0, c.last_layer ? 0 : 1,
-                                  stream)) != SV2_OK)
+        if ((rc = launch_rmsnorm_table(txt, xa, dt, Lt, D, c.norm_eps, tab_ta, tb.ada[0], nullptr,
+                                       c.last_layer ? 0 : 1, stream)) != SV2_OK)
             return rc;
         if ((rc = gemm_rows(stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
             return rc;
@@ -600,28 +625,26 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     if (dbg && ((rc = capture(dbg->attention_vid, att_v, Lv, D)) != SV2_OK ||
                 (Lt > 0 && (rc = capture(dbg->attention_txt, att_t, Lt, D)) != SV2_OK)))
         return rc;
-    // output projections with bias, gated residuals (:1180-1209)
-    if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK ||
-        (rc = launch_bias_rows(p_v, vb.b_proj, dt, Lv, D, stream)) != SV2_OK)
+    // output projections; their bias is added in the gated residual (:1180-1209)
+    if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
         return rc;
-    if (dbg && (rc = capture(dbg->projected_vid, p_v, Lv, D)) != SV2_OK)
+    if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
         return rc;
-    if ((rc = sv2_ada_residual(p_v, vid, dt, Lv, D, emb, vb.ada[2], 0, 0, stream)) != SV2_OK)
+    if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
         return rc;
     if (Lt > 0)
     {
-        if ((rc = gemm_rows(stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK ||
-            (rc = launch_bias_rows(p_t, tb.b_proj, dt, Lt, D, stream)) != SV2_OK)
+        if ((rc = gemm_rows(stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK)
             return rc;
-        if (dbg && (rc = capture(dbg->projected_txt, p_t, Lt, D)) != SV2_OK)
+        if (dbg && (rc = capture_projected(dbg->projected_txt, p_t, tb.b_proj, Lt)) != SV2_OK)
             return rc;
-        rc = c.last_layer ? sv2_ada_residual(p_t, txt, dt, Lt, D, nullptr, nullptr, 0, 1, stream)
-                          : sv2_ada_residual(p_t, txt, dt, Lt, D, emb, tb.ada[2], 0, 0, stream);
-        if (rc != SV2_OK)
+        // the last layer adds the plain residual (:1198-1209)
+        if ((rc = launch_residual_table(p_t, txt, dt, Lt, D, tab_ta, tb.b_proj, c.last_layer ? 1 : 0, stream)) !=
+            SV2_OK)
             return rc;
     }
     // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)
-    if ((rc = branch_mlp(b, stream, vb, emb, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
+    if ((rc = branch_mlp(b, stream, vb, tab_vm, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
         return rc;
     if (Lt > 0)
     {
@@ -631,10 +654,10 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                                             stream);
             if (err != hipSuccess)
                 return hip_error(err, "sv2_block_forward: text copy");
-            if ((rc = sv2_ada_residual(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 0, 2, stream)) != SV2_OK)
+            if ((rc = launch_residual_table(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 2, stream)) != SV2_OK)
                 return rc;
         }
-        else if ((rc = branch_mlp(b, stream, tb, emb, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
+        else if ((rc = branch_mlp(b, stream, tb, tab_tm, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
         {
             return rc;
         }

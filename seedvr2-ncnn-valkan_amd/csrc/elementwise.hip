@@ -17,18 +17,80 @@ using namespace vec;
 // Most 8-element vectors one lane keeps in registers per row (dim <= 8*64*kMaxVec).
 constexpr int kMaxVec = 8;
 
+// Operands of the ada modulation for 8 consecutive channels c0..c0+7.
+//   input:  mul[c] = emb[c*6+slot+1] + scale[c], e0[c] = emb[c*6+slot], sh[c] = shift[c]
+//   output: g[c]   = emb[c*6+slot+2] + gate[c]
+// The reference's emb blob interleaves the six slots per channel ([dim][6]);
+// EmbInput / EmbGate read it as it is (4-byte loads at a 24-byte stride).
+// TableInput / TableGate read per-layer vectors precomputed by ada_table_kernel
+// with the same fp32 additions, as 16-byte loads: the results are identical.
+struct EmbInput
+{
+    const float* emb;
+    const float* shift;
+    const float* scale;
+    int slot;
+    __device__ void load(int c0, float mul[8], float e0[8], float sh[8]) const
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            const int c = c0 + e;
+            mul[e] = emb[c * 6 + slot + 1] + scale[c];
+            e0[e] = emb[c * 6 + slot];
+            sh[e] = shift[c];
+        }
+    }
+};
+
+struct TableInput
+{
+    const float* mul;
+    const float* e0;
+    const float* shift;
+    __device__ void load(int c0, float m[8], float e[8], float sh[8]) const
+    {
+        ld8<F32>(mul, c0, m);
+        ld8<F32>(e0, c0, e);
+        ld8<F32>(shift, c0, sh);
+    }
+};
+
+struct EmbGate
+{
+    const float* emb;
+    const float* gate;
+    int slot;
+    __device__ void load(int c0, float g[8]) const
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            g[e] = emb[(c0 + e) * 6 + slot] + gate[c0 + e];
+    }
+};
+
+struct TableGate
+{
+    const float* g;
+    __device__ void load(int c0, float out[8]) const
+    {
+        ld8<F32>(g, c0, out);
+    }
+};
+
 // One wave per row.  Follows apply_rmsnorm + apply_ada_input
 // (seedvr2_dit_block.cpp:770-805): a double sum of squares, inv =
 // 1/sqrtf(float(ss/dim) + eps), x *= inv, then
 // x = x*(emb[c*6+slot+1] + scale[c]) + emb[c*6+slot] + shift[c] evaluated left
 // to right in fp32 with no fused multiply-add.  With `gamma` (the DiT output
 // head's norm weight, seedvr2_dit_output.cpp:372-384) x = (x * inv) * gamma[c]
-// before the modulation.  The row stays in registers
-// between the reduction and the write, so HBM sees one read and one write.
-template <typename T>
+// before the modulation.  The row stays in registers between the reduction
+// and the write, so HBM sees one read and one write.
+template <typename T, typename Mod>
 __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y, int rows, int dim, float eps,
-                                                          const float* emb, const float* shift, const float* scale,
-                                                          const float* gamma, int slot, int has_ada)
+                                                          Mod mod, const float* gamma, int has_ada)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -61,39 +123,58 @@ __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y
         const int vi = lane + 64 * k;
         if (vi < nvec)
         {
+            const int c0 = vi * 8;
             float out[8];
 #pragma unroll
             for (int e = 0; e < 8; e++)
+                out[e] = v[k][e] * inv;
+            if (gamma)
             {
-                const int c = vi * 8 + e;
-                float t = v[k][e] * inv;
-                if (gamma)
-                    t = t * gamma[c];
-                if (has_ada)
-                {
-                    const float mul = emb[c * 6 + slot + 1] + scale[c];
-                    const float add1 = t * mul;
-                    const float add2 = add1 + emb[c * 6 + slot];
-                    t = add2 + shift[c];
-                }
-                out[e] = t;
+                float gm[8];
+                ld8<F32>(gamma, c0, gm);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    out[e] = out[e] * gm[e];
             }
-            st8<T>(y, base + vi * 8, out);
+            if (has_ada)
+            {
+                float mul[8], e0[8], sh[8];
+                mod.load(c0, mul, e0, sh);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                {
+                    const float add1 = out[e] * mul[e];
+                    const float add2 = add1 + e0[e];
+                    out[e] = add2 + sh[e];
+                }
+            }
+            st8<T>(y, base + c0, out);
         }
     }
 }
 
-// seedvr2_dit_block.cpp:807-825 (mode 0), :1198-1209 (mode 1), :1225-1246 (mode 2).
-template <typename T>
+// seedvr2_dit_block.cpp:807-825 (mode 0), :1198-1209 (mode 1), :1225-1246
+// (mode 2).  With `bias`, x = x + bias[c] first (the bias of the preceding
+// InnerProduct, fused here instead of a pass of its own).
+template <typename T, typename Gate>
 __global__ __launch_bounds__(256) void ada_residual_kernel(void* x, const void* residual, long long count, int dim,
-                                                           const float* emb, const float* gate, int slot, int mode)
+                                                           Gate gate, const float* bias, int mode)
 {
 #pragma clang fp contract(off)
     const long long i = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
     if (i >= count)
         return;
+    const int c0 = static_cast<int>(i % dim);
     float a[8];
     ld8<T>(x, i, a);
+    if (bias)
+    {
+        float b[8];
+        ld8<F32>(bias, c0, b);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            a[e] = a[e] + b[e];
+    }
     float out[8];
     if (mode == 2)
     {
@@ -113,18 +194,34 @@ __global__ __launch_bounds__(256) void ada_residual_kernel(void* x, const void* 
         }
         else
         {
-            const int c0 = static_cast<int>(i % dim);
+            float g[8];
+            gate.load(c0, g);
 #pragma unroll
             for (int e = 0; e < 8; e++)
             {
-                const int c = c0 + e;
-                const float mul = emb[c * 6 + slot] + gate[c];
-                const float t = a[e] * mul;
+                const float t = a[e] * g[e];
                 out[e] = t + r[e];
             }
         }
     }
     st8<T>(x, i, out);
+}
+
+// Per-layer modulation vectors from the emb blob (see EmbInput / EmbGate):
+// out[0][c] = emb[c*6+slot+1] + scale[c], out[1][c] = emb[c*6+slot],
+// out[2][c] = emb[c*6+slot+2] + gate[c] (skipped when gate is NULL), for dim
+// channels.
+__global__ __launch_bounds__(256) void ada_table_kernel(const float* emb, const float* scale, const float* gate,
+                                                        int slot, int dim, float* out)
+{
+#pragma clang fp contract(off)
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= dim)
+        return;
+    out[c] = emb[c * 6 + slot + 1] + scale[c];
+    out[dim + c] = emb[c * 6 + slot];
+    if (gate)
+        out[2 * dim + c] = emb[c * 6 + slot + 2] + gate[c];
 }
 
 // silu(g) * v with silu(g) = g / (1 + exp(-g)) (seedvr2_dit_block.cpp:58-61, :1103-1109).
@@ -232,24 +329,70 @@ int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipSt
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "to_f32_kernel launch");
 }
-int launch_rmsnorm_ada(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* emb,
-                       const float* shift, const float* scale, const float* gamma, int slot_base, int has_ada,
-                       hipStream_t stream)
+template <typename Mod>
+int launch_rmsnorm(const void* x, void* y, int dtype, int rows, int dim, float eps, Mod mod, const float* gamma,
+                   int has_ada, hipStream_t stream)
 {
     if (rows == 0)
         return SV2_OK;
     const dim3 grid((rows + 3) / 4);
     if (dtype == SV2_F32)
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<F32>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
-                           gamma, slot_base, has_ada);
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
+                           gamma, has_ada);
     else if (dtype == SV2_F16)
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<F16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift, scale,
-                           gamma, slot_base, has_ada);
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
+                           gamma, has_ada);
     else
-        hipLaunchKernelGGL(rmsnorm_ada_kernel<BF16>, grid, dim3(256), 0, stream, x, y, rows, dim, eps, emb, shift,
-                           scale, gamma, slot_base, has_ada);
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
+                           gamma, has_ada);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
+}
+
+template <typename Gate>
+int launch_residual(void* x, const void* residual, int dtype, int rows, int dim, Gate gate, const float* bias,
+                    int mode, hipStream_t stream)
+{
+    const long long count = static_cast<long long>(rows) * dim;
+    if (count == 0)
+        return SV2_OK;
+    const dim3 grid(static_cast<unsigned>((count / 8 + 255) / 256));
+    if (dtype == SV2_F32)
+        hipLaunchKernelGGL((ada_residual_kernel<F32, Gate>), grid, dim3(256), 0, stream, x, residual, count, dim,
+                           gate, bias, mode);
+    else if (dtype == SV2_F16)
+        hipLaunchKernelGGL((ada_residual_kernel<F16, Gate>), grid, dim3(256), 0, stream, x, residual, count, dim,
+                           gate, bias, mode);
+    else
+        hipLaunchKernelGGL((ada_residual_kernel<BF16, Gate>), grid, dim3(256), 0, stream, x, residual, count, dim,
+                           gate, bias, mode);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "ada_residual_kernel launch");
+}
+
+int launch_ada_table(const float* emb, const float* scale, const float* gate, int slot, int dim, float* out,
+                     hipStream_t stream)
+{
+    if (dim <= 0 || dim % 8 != 0 || (slot != 0 && slot != 3))
+        return set_error(SV2_EINVAL, "ada_table: bad dim or slot");
+    hipLaunchKernelGGL(ada_table_kernel, dim3((dim + 255) / 256), dim3(256), 0, stream, emb, scale, gate, slot, dim,
+                       out);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "ada_table_kernel launch");
+}
+
+int launch_rmsnorm_table(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* table,
+                         const float* shift, const float* gamma, int has_ada, hipStream_t stream)
+{
+    const TableInput mod{table, table ? table + dim : nullptr, shift};
+    return launch_rmsnorm(x, y, dtype, rows, dim, eps, mod, gamma, has_ada, stream);
+}
+
+int launch_residual_table(void* x, const void* residual, int dtype, int rows, int dim, const float* table,
+                          const float* bias, int mode, hipStream_t stream)
+{
+    const TableGate gate{table ? table + 2 * dim : nullptr};
+    return launch_residual(x, residual, dtype, rows, dim, gate, bias, mode, stream);
 }
 } // namespace sv2
 
@@ -269,12 +412,12 @@ int sv2_rmsnorm_ada(const void* x, void* y, int io_dtype, int rows, int dim, flo
         return set_error(SV2_EINVAL, "rmsnorm_ada: null pointer");
     if (slot_base != 0 && slot_base != 3)
         return set_error(SV2_EINVAL, "rmsnorm_ada: slot_base must be 0 or 3");
-    return launch_rmsnorm_ada(x, y, io_dtype, rows, dim, eps, emb, shift, scale, nullptr, slot_base, has_ada,
-                              static_cast<hipStream_t>(stream_ptr));
+    const EmbInput mod{emb, shift, scale, slot_base};
+    return launch_rmsnorm(x, y, io_dtype, rows, dim, eps, mod, nullptr, has_ada, static_cast<hipStream_t>(stream_ptr));
 }
 
 int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int dim, const float* emb,
-                     const float* gate, int slot_base, int mode, void* stream_ptr)
+                     const float* gate_vec, int slot_base, int mode, void* stream_ptr)
 {
     using namespace sv2;
     if (!dtype_ok(io_dtype) || rows < 0 || dim <= 0 || mode < 0 || mode > 2)
@@ -283,25 +426,12 @@ int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int 
         return set_error(SV2_EUNSUPPORTED, "ada_residual: dim must be a multiple of 8");
     if (rows == 0)
         return SV2_OK;
-    if (!x || (mode != 2 && !residual) || (mode == 0 && (!emb || !gate)))
+    if (!x || (mode != 2 && !residual) || (mode == 0 && (!emb || !gate_vec)))
         return set_error(SV2_EINVAL, "ada_residual: null pointer");
     if (slot_base != 0 && slot_base != 3)
         return set_error(SV2_EINVAL, "ada_residual: slot_base must be 0 or 3");
-    const long long count = static_cast<long long>(rows) * dim;
-    const dim3 grid(static_cast<unsigned>((count / 8 + 255) / 256));
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const int slot = slot_base + 2;
-    if (io_dtype == SV2_F32)
-        hipLaunchKernelGGL(ada_residual_kernel<F32>, grid, dim3(256), 0, stream, x, residual, count, dim, emb, gate,
-                           slot, mode);
-    else if (io_dtype == SV2_F16)
-        hipLaunchKernelGGL(ada_residual_kernel<F16>, grid, dim3(256), 0, stream, x, residual, count, dim, emb, gate,
-                           slot, mode);
-    else
-        hipLaunchKernelGGL(ada_residual_kernel<BF16>, grid, dim3(256), 0, stream, x, residual, count, dim, emb, gate,
-                           slot, mode);
-    const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? SV2_OK : hip_error(err, "ada_residual_kernel launch");
+    const EmbGate gate{emb, gate_vec, slot_base + 2};
+    return launch_residual(x, residual, io_dtype, rows, dim, gate, nullptr, mode, static_cast<hipStream_t>(stream_ptr));
 }
 
 int sv2_swiglu(void* gate, const void* value, int io_dtype, int64_t count, void* stream_ptr)

@@ -111,11 +111,20 @@ int launch_bias_rows(void* y, const float* b, int dtype, int rows, int cols, hip
 // The same, then y = silu(y) when `silu` is non-zero.
 int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int silu, hipStream_t stream);
 
-// Token RMSNorm (optionally times gamma[c]) and ada modulation; the
-// arguments of sv2_rmsnorm_ada, already validated, plus `gamma` (may be NULL).
-int launch_rmsnorm_ada(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* emb,
-                       const float* shift, const float* scale, const float* gamma, int slot_base, int has_ada,
-                       hipStream_t stream);
+// Per-layer ada modulation table [3][dim] from the emb blob [dim][6]:
+// row 0 emb[c*6+slot+1] + scale[c], row 1 emb[c*6+slot], row 2
+// emb[c*6+slot+2] + gate[c] (slot 0 attention, 3 MLP).
+int launch_ada_table(const float* emb, const float* scale, const float* gate, int slot, int dim, float* out,
+                     hipStream_t stream);
+// Token RMSNorm (times gamma[c] when gamma is not NULL), then when has_ada
+// the input modulation with rows 0-1 of `table` and `shift`.  Arguments
+// already validated (dim a multiple of 8, <= 4096).
+int launch_rmsnorm_table(const void* x, void* y, int dtype, int rows, int dim, float eps, const float* table,
+                         const float* shift, const float* gamma, int has_ada, hipStream_t stream);
+// x = (x [+ bias]) * table[2] + residual (mode 0), x + residual (mode 1),
+// 2x (mode 2); bias may be NULL.
+int launch_residual_table(void* x, const void* residual, int dtype, int rows, int dim, const float* table,
+                          const float* bias, int mode, hipStream_t stream);
 
 // y[rows, out] = x[rows, in] W^T, W [out][in] row-major (an InnerProduct
 // without its bias), in dtype (SV2_F32 or SV2_F16) with fp32 accumulation,
