@@ -1162,6 +1162,86 @@ __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const
         }
 }
 
+// Bytes per row of the epilogue staging area: 256 B of outputs + 16 B, so the
+// rows of one store wave start on different LDS banks.
+constexpr int kEpiStride = 272;
+
+// Epilogue of one wave for 16-bit outputs: the wave's 32 x 128 tile of
+// rounded outputs (as write_outputs rounds them) is staged in LDS, then every
+// 256-byte output row segment is stored by 16 lanes with one 16-byte store
+// each, instead of sixteen 8-byte pieces from two lanes.  Every lane of the
+// wave takes part (rows at or past q_end are staged but not stored).
+__device__ inline void write_outputs_lds(const AttnParams& p, const Staged& s, const WindowBox& box, int wi,
+                                         int head, int q_wave0, int q_end, int lane, const f32x16 o[4],
+                                         float inv_l, char* stage)
+{
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    const int lr = lane & 31;
+    const int g = lane >> 5;
+    const int qrow = q_wave0 + lr;
+    const bool text = qrow >= box.vlen;
+    const bool f16_out = !text && p.out_dtype == SV2_F16;
+    const long long pre_row =
+        (static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len + qrow) * p.dim +
+        static_cast<long long>(head) * kHeadDim;
+    char* my_row = stage + lr * kEpiStride;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++)
+        {
+            const int d = dt * 32 + 8 * rq + 4 * g;
+            float pre[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                pre[e] = o[dt][4 * rq + e] * inv_l;
+            if (p.dbg_pre && qrow < q_end)
+                store4<F32>(p.dbg_pre, pre_row + d, pre);
+            bf16x2 a;
+            bf16x2 b;
+            a[0] = static_cast<__bf16>(pre[0]);
+            a[1] = static_cast<__bf16>(pre[1]);
+            b[0] = static_cast<__bf16>(pre[2]);
+            b[1] = static_cast<__bf16>(pre[3]);
+            uint32_t lo = __builtin_bit_cast(uint32_t, a);
+            uint32_t hi = __builtin_bit_cast(uint32_t, b);
+            if (f16_out)
+            {
+                // the bf16 values are exact in fp16 within its range
+                f16x2 fa, fb;
+                fa[0] = static_cast<_Float16>(__builtin_bit_cast(float, lo << 16));
+                fa[1] = static_cast<_Float16>(__builtin_bit_cast(float, lo & 0xffff0000u));
+                fb[0] = static_cast<_Float16>(__builtin_bit_cast(float, hi << 16));
+                fb[1] = static_cast<_Float16>(__builtin_bit_cast(float, hi & 0xffff0000u));
+                lo = __builtin_bit_cast(uint32_t, fa);
+                hi = __builtin_bit_cast(uint32_t, fb);
+            }
+            *reinterpret_cast<uint2*>(my_row + 2 * d) = make_uint2(lo, hi);
+        }
+    // the rows are read back by other lanes of this wave: LDS operations of a
+    // wave complete in order, and the wait makes the compiler keep it so
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    const int chunk = lane & 15;
+    const long long col = static_cast<long long>(head) * kHeadDim + chunk * 8;
+#pragma unroll
+    for (int it = 0; it < 8; it++)
+    {
+        const int rl = it * 4 + (lane >> 4);
+        const int q = q_wave0 + rl;
+        if (q < q_end)
+        {
+            const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kEpiStride + chunk * 16);
+            uint16_t* dst;
+            if (q < box.vlen)
+                dst = static_cast<uint16_t*>(p.vid_out) + static_cast<long long>(s.rows[q].x) * p.dim + col;
+            else
+                dst = p.partial + (static_cast<long long>(wi) * p.text_len + (q - box.vlen)) * p.dim + col;
+            *reinterpret_cast<uint4*>(dst) = v;
+        }
+    }
+}
+
 template <typename TI, int RM>
 __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p)
 {
@@ -1283,6 +1363,17 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     if (!wave_active)
         return;
     const float l_tot = partner_sum(l_run);
+    if constexpr (TI::kDma)
+    {
+        // 16-bit outputs leave through LDS (the tile buffers are free: every
+        // wave passed the loop's last barrier and every fetch has landed)
+        if (p.out_dtype != SV2_F32)
+        {
+            write_outputs_lds(p, s, box, wi, head, qbk.q0 + wave * 32, qbk.q1, lane, o, 1.f / l_tot,
+                              smem + p.lds.k + wave * 32 * kEpiStride);
+            return;
+        }
+    }
     if (qrow >= qbk.q1)
         return;
     write_outputs(p, s, box, wi, head, qrow, g, o, 1.f / l_tot);
@@ -1551,6 +1642,7 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
     if (qkv_elems >= (int64_t(1) << 40))
         return set_error(SV2_EUNSUPPORTED, "attention: qkv tensor too large");
     p->lds = lds_layout(vmax, rope_rows, a->qkv_dtype != SV2_F32);
+    static_assert(kWaves * 32 * kEpiStride <= 7 * kTileBytes, "epilogue staging must fit the tile buffers");
     if (p->lds.total > kMaxLds)
         return set_error(SV2_EUNSUPPORTED, "attention: the window's staged tables exceed the LDS of a CU");
     p->vid_qkv = a->vid_qkv;
