@@ -1,10 +1,19 @@
-// Matrix products of the InnerProduct layers on rocBLAS, one handle per
-// device for the whole process.
+// Matrix products of the InnerProduct layers.
+//
+// fp16 (the fast mode): hipBLASLt with fp32 accumulation.  The first product
+// of a shape on a device asks the library for its 16 best-ranked kernels that
+// need no workspace, times each on the caller's stream with the caller's
+// buffers and keeps the fastest for the rest of the process; that first call
+// therefore synchronises the stream once.  Without a workspace, products on
+// different streams share nothing.
+// fp32 (the parity mode): rocBLAS gemm_ex.
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 
 #include "sv2_internal.h"
 
@@ -13,30 +22,185 @@ namespace sv2
 namespace
 {
 
-// One rocBLAS handle per device, shared by every layer of the process.
-rocblas_handle blas_handle(int* rc)
+std::mutex g_mutex;
+
+int current_device(int* rc)
 {
-    static std::mutex mutex;
-    static std::map<int, rocblas_handle> handles;
     int device = 0;
-    hipError_t err = hipGetDevice(&device);
+    const hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess)
     {
-        *rc = sv2::hip_error(err, "gemm: hipGetDevice");
-        return nullptr;
+        *rc = hip_error(err, "gemm: hipGetDevice");
+        return -1;
     }
-    std::lock_guard<std::mutex> lock(mutex);
+    return device;
+}
+
+// One rocBLAS handle per device (caller holds g_mutex).
+rocblas_handle rocblas_for(int device, int* rc)
+{
+    static std::map<int, rocblas_handle> handles;
     auto it = handles.find(device);
     if (it != handles.end())
         return it->second;
     rocblas_handle h = nullptr;
     if (rocblas_create_handle(&h) != rocblas_status_success)
     {
-        *rc = sv2::set_error(SV2_EDEVICE, "gemm: rocblas_create_handle failed");
+        *rc = set_error(SV2_EDEVICE, "gemm: rocblas_create_handle failed");
         return nullptr;
     }
     handles[device] = h;
     return h;
+}
+
+// One hipBLASLt handle per device (caller holds g_mutex).
+hipblasLtHandle_t lt_for(int device, int* rc)
+{
+    static std::map<int, hipblasLtHandle_t> handles;
+    auto it = handles.find(device);
+    if (it != handles.end())
+        return it->second;
+    hipblasLtHandle_t h = nullptr;
+    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS)
+    {
+        *rc = set_error(SV2_EDEVICE, "gemm: hipblasLtCreate failed");
+        return nullptr;
+    }
+    handles[device] = h;
+    return h;
+}
+
+// A tuned fp16 product: column-major D[out x rows] = op(A) B with A = W
+// stored [out][in] row-major (in x out, transposed), B = X [rows][in]
+// row-major (in x rows), D = Y [rows][out] row-major (out x rows).
+struct LtPlan
+{
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr;
+    hipblasLtMatrixLayout_t b = nullptr;
+    hipblasLtMatrixLayout_t d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+using PlanKey = std::tuple<int, int, int, int>; // device, rows, in, out
+
+int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out, const void* x, const void* w,
+              void* y, LtPlan* plan)
+{
+    if (hipblasLtMatmulDescCreate(&plan->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+        return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmulDescCreate failed");
+    const hipblasOperation_t ta = HIPBLAS_OP_T;
+    const hipblasOperation_t tb = HIPBLAS_OP_N;
+    if (hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&plan->a, HIP_R_16F, in, out, in) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&plan->b, HIP_R_16F, in, rows, in) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&plan->d, HIP_R_16F, out, rows, out) != HIPBLAS_STATUS_SUCCESS)
+        return set_error(SV2_EDEVICE, "gemm: hipBLASLt descriptor setup failed");
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS)
+        return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmulPreferenceCreate failed");
+    const uint64_t no_workspace = 0;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
+                                          sizeof(no_workspace));
+    constexpr int kCandidates = 16;
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
+    int got = 0;
+    const hipblasStatus_t hs =
+        hipblasLtMatmulAlgoGetHeuristic(h, plan->desc, plan->a, plan->b, plan->d, plan->d, pref, kCandidates, res, &got);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (hs != HIPBLAS_STATUS_SUCCESS || got <= 0)
+        return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no kernel for an fp16 product of this shape");
+    const float alpha = 1.f;
+    const float beta = 0.f;
+    hipEvent_t e0 = nullptr;
+    hipEvent_t e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        return set_error(SV2_EDEVICE, "gemm: hipEventCreate failed");
+    float best = -1.f;
+    for (int i = 0; i < got; i++)
+    {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize != 0)
+            continue;
+        bool ok = hipblasLtMatmul(h, plan->desc, &alpha, w, plan->a, x, plan->b, &beta, y, plan->d, y, plan->d,
+                                  &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipEventRecord(e0, stream) == hipSuccess;
+        for (int r = 0; r < 3 && ok; r++)
+            ok = hipblasLtMatmul(h, plan->desc, &alpha, w, plan->a, x, plan->b, &beta, y, plan->d, y, plan->d,
+                                 &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+        float ms = 0.f;
+        if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+            continue;
+        if (best < 0.f || ms < best)
+        {
+            best = ms;
+            plan->algo = res[i].algo;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (best < 0.f)
+        return set_error(SV2_EDEVICE, "gemm: no hipBLASLt kernel ran for an fp16 product of this shape");
+    return SV2_OK;
+}
+
+int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y)
+{
+    int rc = SV2_OK;
+    LtPlan plan;
+    hipblasLtHandle_t h = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        const int device = current_device(&rc);
+        if (device < 0)
+            return rc;
+        h = lt_for(device, &rc);
+        if (!h)
+            return rc;
+        static std::map<PlanKey, LtPlan> plans;
+        const PlanKey key{device, rows, in, out};
+        auto it = plans.find(key);
+        if (it == plans.end())
+        {
+            LtPlan fresh;
+            if ((rc = make_plan(h, stream, rows, in, out, x, w, y, &fresh)) != SV2_OK)
+                return rc;
+            it = plans.emplace(key, fresh).first;
+        }
+        plan = it->second;
+    }
+    const float alpha = 1.f;
+    const float beta = 0.f;
+    if (hipblasLtMatmul(h, plan.desc, &alpha, w, plan.a, x, plan.b, &beta, y, plan.d, y, plan.d, &plan.algo, nullptr,
+                        0, stream) != HIPBLAS_STATUS_SUCCESS)
+        return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmul failed");
+    return SV2_OK;
+}
+
+int gemm_f32(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y)
+{
+    int rc = SV2_OK;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    const int device = current_device(&rc);
+    if (device < 0)
+        return rc;
+    rocblas_handle h = rocblas_for(device, &rc);
+    if (!h)
+        return rc;
+    const float alpha = 1.f;
+    const float beta = 0.f;
+    rocblas_set_stream(h, stream);
+    // column-major view: Y^T [out x rows] = W [out x in] * X^T [in x rows]
+    const rocblas_status st =
+        rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, out, rows, in, &alpha, w,
+                        rocblas_datatype_f32_r, in, x, rocblas_datatype_f32_r, in, &beta, y, rocblas_datatype_f32_r,
+                        out, y, rocblas_datatype_f32_r, out, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return set_error(SV2_EDEVICE, std::string("gemm: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+    return SV2_OK;
 }
 
 } // namespace
@@ -45,21 +209,11 @@ int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const vo
 {
     if (rows == 0)
         return SV2_OK;
-    int rc = SV2_OK;
-    rocblas_handle h = blas_handle(&rc);
-    if (!h)
-        return rc;
-    const rocblas_datatype t = dtype == SV2_F32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
-    const float alpha = 1.f;
-    const float beta = 0.f;
-    rocblas_set_stream(h, stream);
-    // column-major view: Y^T [out x rows] = W [out x in] * X^T [in x rows]
-    const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, out, rows, in,
-                                              &alpha, w, t, in, x, t, in, &beta, y, t, out, y, t, out,
-                                              rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return sv2::set_error(SV2_EDEVICE, std::string("gemm: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
-    return SV2_OK;
+    if (dtype == SV2_F16)
+        return gemm_f16(stream, rows, in, out, x, w, y);
+    if (dtype == SV2_F32)
+        return gemm_f32(stream, rows, in, out, x, w, y);
+    return set_error(SV2_EINVAL, "gemm: compute dtype must be fp32 or fp16");
 }
 
 } // namespace sv2

@@ -127,8 +127,10 @@ int launch_residual_table(void* x, const void* residual, int dtype, int rows, in
                           const float* bias, int mode, hipStream_t stream);
 
 // y[rows, out] = x[rows, in] W^T, W [out][in] row-major (an InnerProduct
-// without its bias), in dtype (SV2_F32 or SV2_F16) with fp32 accumulation,
-// on rocBLAS; enqueued on `stream`.
+// without its bias), in dtype (SV2_F32 or SV2_F16) with fp32 accumulation;
+// enqueued on `stream`.  fp16 runs on hipBLASLt (the first product of a shape
+// times the library's candidate kernels and synchronises the stream once),
+// fp32 on rocBLAS.
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y);
 
 // Allocates device memory for `count` host fp32 values, stores them as dtype
