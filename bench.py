@@ -197,6 +197,50 @@ def dit_bench(dev, steps: int, warmup: int):
     }
 
 
+def sampler_bench(dev, reps: int = 50):
+    """The sampler half of one Euler step at 1280x720x21 (latent 16x6x90x160,
+    fp32, resident): the 33-channel DiT input, CFG 6.5 with rescale 0.7 of two
+    predictions, and the Euler update; per operation the mean time over
+    `reps` launches and its algorithmic HBM bytes (each element read and
+    written once per pass: DiT input 65 x 4 B per token, CFG 12 B + the
+    rescale pass 8 B per element, Euler 12 B per element)."""
+    import torch
+    import sv2hip
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    shape = (16, T, 2 * H, 2 * W)
+    n = 16 * T * 4 * H * W
+    lat, cond, pos, neg = (torch.randn(shape, generator=g, device=dev) for _ in range(4))
+    s = sv2hip.EulerSampler(50)
+    dit_in = torch.empty((33,) + shape[1:], device=dev)
+    guided = torch.empty_like(lat)
+    nxt = torch.empty_like(lat)
+    stream = torch.cuda.current_stream()
+    ops = {
+        "dit_input": (lambda: s.make_dit_input(lat, cond, output=dit_in, stream=stream), 65 * 4 * n // 16),
+        "cfg_rescale": (lambda: s.apply_cfg(pos, neg, 6.5, 0.7, output=guided, stream=stream), 20 * n),
+        "euler_step": (lambda: s.step_to(guided, lat, 980.0, 960.0, output=nxt, stream=stream), 12 * n),
+    }
+    out = {}
+    for name, (fn, nbytes) in ops.items():
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "hbm_util": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    out["step_us"] = round(sum(v["us"] for v in out.values()), 2)
+    out["workload"] = "sampler step at 1280x720x21: latent 16x6x90x160 fp32, CFG 6.5 rescale 0.7, Euler 980->960"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +250,8 @@ def main():
     ap.add_argument("--dit-steps", type=int, default=3, help="timed DiT forwards (0 skips the DiT leg)")
     ap.add_argument("--dit-only", action="store_true",
                     help="run only the DiT leg and print its figures (for profiling the DiT step)")
+    ap.add_argument("--sampler-only", action="store_true",
+                    help="run only the sampler leg and print its figures (for profiling the sampler kernels)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a device buffer of BYTES three times (a plain copy kernel of known "
                          "size, to calibrate the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -228,6 +274,9 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
         return
     sv2hip.load()
+    if args.sampler_only:
+        print(json.dumps({"sampler_step": sampler_bench(dev)}))
+        return
     if args.dit_only:
         print(json.dumps({"dit_step": dit_bench(dev, max(args.dit_steps, 1), 1)}))
         return
@@ -315,6 +364,7 @@ def main():
             "variants": variants,
             "dit_step_ms": None,
             "dit_step": None,
+            "sampler_step": None,
         },
         "roofline": {
             "bound": "hbm",
@@ -329,6 +379,7 @@ def main():
         ds = dit_bench(dev, args.dit_steps, 1)
         result["config"]["dit_step_ms"] = ds["ms"]
         result["config"]["dit_step"] = ds
+    result["config"]["sampler_step"] = sampler_bench(dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))

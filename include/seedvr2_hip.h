@@ -408,6 +408,56 @@ int sv2_dit_forward(sv2_dit* dit, const float* latent, const float* text, int te
                     int height, int width, float* output, void* workspace, size_t workspace_bytes, void* stream);
 void sv2_dit_destroy(sv2_dit* dit);
 
+/* ---- Euler sampler (src/model/sampler.h:18-78) and the latent preparation
+ * of the engine loop (src/core/engine.cpp:79-149, :306-350).  Latents are
+ * fp32 device arrays treated as flat element sequences except where a layout
+ * is named.  Every operation evaluates the reference's float expression in
+ * the same order without fused multiply-adds, so outputs are bit-identical
+ * to the reference's CPU sampler; the guidance rescale factor is formed from
+ * double sums in a fixed order and can differ from the reference's by an
+ * ulp of the factor. */
+
+/* Host.  The schedule of EulerSampler::EulerSampler (sampler.cpp:181-187):
+ * steps <= 0 counts as 1; out[i] = 1000 * (1 - i / steps).  `out` holds
+ * max(1, steps) floats; returns that count, or SV2_EINVAL. */
+int sv2_euler_timesteps(int steps, float* out);
+/* Host.  The condition noise ratio of make_condition_latent (engine.cpp:79-92
+ * and :110): transformed_condition_timestep(noise_scale) / 1000 for an
+ * encoded latent of frames x height x width. */
+float sv2_condition_ratio(float noise_scale, int frames, int height, int width);
+/* out = (1 - ratio) * encoded + ratio * noise, elementwise over `count`
+ * floats (make_condition_latent, engine.cpp:106-122;
+ * EulerSampler::make_condition_vulkan, sampler.h:45-51). */
+int sv2_make_condition(const float* encoded, const float* noise, float* out, int64_t count, float ratio,
+                       void* stream);
+/* The 33-channel DiT input: channels 0-15 the latent, 16-31 the condition,
+ * 32 ones.  channel_major != 0: [16][tokens] sources, [33][tokens] output
+ * (make_dit_input, engine.cpp:125-149); 0: [tokens][16] sources,
+ * [tokens][33] output (EulerSampler::make_dit_input_vulkan,
+ * sampler.cpp:337-357). */
+int sv2_make_dit_input(const float* latent, const float* condition, float* out, int64_t tokens, int channel_major,
+                       void* stream);
+/* Workspace bytes of sv2_apply_cfg with a non-zero rescale (a few KiB). */
+int64_t sv2_cfg_workspace_size(int64_t count);
+/* Classifier-free guidance (EulerSampler::apply_cfg, sampler.cpp:201-236;
+ * apply_cfg_vulkan, sampler.h:58-65): out = neg + scale * (pos - neg); when
+ * rescale != 0 and the unbiased standard deviation of out is positive, out is
+ * multiplied by float(rescale * std(pos) / std(out) + (1 - rescale)).  The
+ * statistics are reduced on the device (no host synchronisation); the
+ * workspace is needed only when rescale != 0.  `out` may alias either
+ * input (each element is read before it is written, by the same thread). */
+int sv2_apply_cfg(const float* positive, const float* negative, float* out, int64_t count, float scale,
+                  float rescale, void* workspace, size_t workspace_bytes, void* stream);
+/* The Euler / v-lerp update (EulerSampler::step_to, sampler.cpp:239-265):
+ * with bt = t / 1000, at = 1 - bt, bs = clamp(t_next / 1000, 0, 1),
+ * as = 1 - bs: out = as * (x - bt * pred) + bs * (x + at * pred). */
+int sv2_euler_step(const float* prediction, const float* current, float* out, int64_t count, float timestep,
+                   float next_timestep, void* stream);
+/* The last step (EulerSampler::endpoint, sampler.cpp:267-285):
+ * out = x - (t / 1000) * pred. */
+int sv2_euler_endpoint(const float* prediction, const float* current, float* out, int64_t count, float timestep,
+                       void* stream);
+
 /* Message of the last failure on the calling thread (never NULL). */
 const char* sv2_last_error(void);
 

@@ -114,6 +114,18 @@ def load() -> ctypes.CDLL:
     lib.orc_dit_input_forward.restype = i
     lib.orc_dit_output_forward.argtypes = [ctypes.POINTER(OrcDitOutput), vp, vp, i, i, i, vp]
     lib.orc_dit_output_forward.restype = i
+    i64, f = ctypes.c_int64, ctypes.c_float
+    lib.orc_euler_timesteps.argtypes = [i, vp]
+    lib.orc_euler_timesteps.restype = i
+    lib.orc_condition_ratio.argtypes = [f, i, i, i]
+    lib.orc_condition_ratio.restype = f
+    lib.orc_make_condition.argtypes = [vp, vp, vp, i64, f]
+    lib.orc_make_dit_input.argtypes = [vp, vp, vp, i64, i]
+    lib.orc_standard_deviation.argtypes = [vp, i64]
+    lib.orc_standard_deviation.restype = ctypes.c_double
+    lib.orc_apply_cfg.argtypes = [vp, vp, vp, i64, f, f]
+    lib.orc_euler_step.argtypes = [vp, vp, vp, i64, f, f]
+    lib.orc_euler_endpoint.argtypes = [vp, vp, vp, i64, f]
     _lib = lib
     return lib
 
@@ -359,3 +371,69 @@ def dit_forward(input_weights, blocks, output_weights, latent, text, timestep, *
     out = dit_output_forward(output_weights, vid, emb, T, H // 2, W // 2, eps=eps, threads=threads)
     oc = out.shape[1]
     return np.ascontiguousarray(np.transpose(out.reshape(T, H, W, oc), (3, 0, 1, 2)))  # dit.cpp:82-95
+
+
+# ---- Euler sampler (src/model/sampler.cpp, src/core/engine.cpp) -----------
+
+def euler_timesteps(steps):
+    """EulerSampler(steps).timesteps() (sampler.cpp:181-187)."""
+    out = np.zeros(max(1, steps), np.float32)
+    n = load().orc_euler_timesteps(steps, _p(out))
+    return out[:n]
+
+
+def condition_ratio(noise_scale, T, H, W):
+    """transformed_condition_timestep / 1000 (engine.cpp:79-92, :110)."""
+    return load().orc_condition_ratio(noise_scale, T, H, W)
+
+
+def make_condition(encoded, noise, ratio):
+    """make_condition_latent (engine.cpp:106-122), any shape."""
+    a, b = _f32(encoded), _f32(noise)
+    out = np.empty_like(a)
+    load().orc_make_condition(_p(a), _p(b), _p(out), a.size, ratio)
+    return out
+
+
+def make_dit_input(latent, condition, channel_major=True):
+    """make_dit_input (engine.cpp:125-149): [16, T, H, W] -> [33, T, H, W];
+    channel_major=False: [tokens, 16] -> [tokens, 33] (sampler.cpp:337-357)."""
+    a, b = _f32(latent), _f32(condition)
+    if channel_major:
+        tokens = a.size // 16
+        out = np.empty((33,) + a.shape[1:], np.float32)
+    else:
+        tokens = a.shape[0]
+        out = np.empty((tokens, 33), np.float32)
+    load().orc_make_dit_input(_p(a), _p(b), _p(out), tokens, 1 if channel_major else 0)
+    return out
+
+
+def standard_deviation(x):
+    """standard_deviation (sampler.cpp:41-62)."""
+    a = _f32(x)
+    return load().orc_standard_deviation(_p(a), a.size)
+
+
+def apply_cfg(positive, negative, scale, rescale):
+    """EulerSampler::apply_cfg (sampler.cpp:201-236)."""
+    a, b = _f32(positive), _f32(negative)
+    out = np.empty_like(a)
+    load().orc_apply_cfg(_p(a), _p(b), _p(out), a.size, scale, rescale)
+    return out
+
+
+def euler_step(prediction, current, timestep, next_timestep):
+    """EulerSampler::step_to (sampler.cpp:239-265)."""
+    a, b = _f32(prediction), _f32(current)
+    out = np.empty_like(b)
+    load().orc_euler_step(_p(a), _p(b), _p(out), b.size, timestep, next_timestep)
+    return out
+
+
+def euler_endpoint(prediction, current, timestep):
+    """EulerSampler::endpoint (sampler.cpp:267-285)."""
+    a, b = _f32(prediction), _f32(current)
+    out = np.empty_like(b)
+    load().orc_euler_endpoint(_p(a), _p(b), _p(out), b.size, timestep)
+    return out

@@ -786,3 +786,108 @@ int orc_dit_output_forward(const orc_dit_output* o, const float* vid, const floa
     free(proj);
     return 0;
 }
+
+/* ---- Euler sampler ---------------------------------------------------- */
+
+int orc_euler_timesteps(int steps, float* out)
+{
+    /* sampler.cpp:181-187 */
+    const int n = steps < 1 ? 1 : steps;
+    for (int i = 0; i < n; i++)
+        out[i] = 1000.0f * (1.0f - (float)i / n);
+    return n;
+}
+
+float orc_condition_ratio(float noise_scale, int T, int H, int W)
+{
+    /* engine.cpp:79-92: latent frames/height/width mapped back to pixels */
+    const float timestep = noise_scale * 1000.0f;
+    if (timestep == 0.0f)
+        return 0.0f;
+    const float frames = (float)((T - 1) * 4 + 1);
+    const float height = (float)(H * 8);
+    const float width = (float)(W * 8);
+    const float x1 = 256.0f * 256.0f * 37.0f;
+    const float x2 = 1280.0f * 720.0f * 145.0f;
+    const float shift = 1.0f + (height * width * frames - x1) * (5.0f - 1.0f) / (x2 - x1);
+    const float normalized = timestep / 1000.0f;
+    const float transformed = 1000.0f * shift * normalized / (1.0f + (shift - 1.0f) * normalized);
+    return transformed / 1000.0f; /* engine.cpp:110 */
+}
+
+void orc_make_condition(const float* encoded, const float* noise, float* out, int64_t count, float ratio)
+{
+    /* engine.cpp:117-118 */
+    for (int64_t i = 0; i < count; i++)
+        out[i] = (1.0f - ratio) * encoded[i] + ratio * noise[i];
+}
+
+void orc_make_dit_input(const float* latent, const float* condition, float* out, int64_t tokens, int channel_major)
+{
+    for (int64_t t = 0; t < tokens; t++)
+        for (int c = 0; c < 33; c++)
+        {
+            float v;
+            if (channel_major) /* engine.cpp:127-147 */
+                v = c < 16 ? latent[c * tokens + t] : c < 32 ? condition[(c - 16) * tokens + t] : 1.0f;
+            else /* [tokens][16] -> [tokens][33] */
+                v = c < 16 ? latent[t * 16 + c] : c < 32 ? condition[t * 16 + c - 16] : 1.0f;
+            out[channel_major ? c * tokens + t : t * 33 + c] = v;
+        }
+}
+
+double orc_standard_deviation(const float* x, int64_t count)
+{
+    /* sampler.cpp:41-62 */
+    double sum = 0.0, square_sum = 0.0;
+    for (int64_t i = 0; i < count; i++)
+    {
+        sum += x[i];
+        square_sum += (double)x[i] * x[i];
+    }
+    if (count <= 1)
+        return 0.0;
+    double variance = (square_sum - sum * sum / count) / (count - 1);
+    if (variance < 0.0)
+        variance = 0.0;
+    return sqrt(variance);
+}
+
+void orc_apply_cfg(const float* pos, const float* neg, float* out, int64_t count, float scale, float rescale)
+{
+    /* sampler.cpp:217-235 */
+    for (int64_t i = 0; i < count; i++)
+        out[i] = neg[i] + scale * (pos[i] - neg[i]);
+    if (rescale == 0.0f)
+        return;
+    const double cfg_std = orc_standard_deviation(out, count);
+    if (!(cfg_std > 0.0))
+        return;
+    const float factor = (float)(rescale * orc_standard_deviation(pos, count) / cfg_std + (1.0f - rescale));
+    for (int64_t i = 0; i < count; i++)
+        out[i] *= factor;
+}
+
+void orc_euler_step(const float* pred, const float* x, float* out, int64_t count, float t, float t_next)
+{
+    /* sampler.cpp:253-263 */
+    const float bt = t / 1000.0f;
+    const float at = 1.0f - bt;
+    float bs = t_next / 1000.0f;
+    bs = bs < 0.0f ? 0.0f : (bs > 1.0f ? 1.0f : bs);
+    const float as = 1.0f - bs;
+    for (int64_t i = 0; i < count; i++)
+    {
+        const float x0 = x[i] - bt * pred[i];
+        const float xT = x[i] + at * pred[i];
+        out[i] = as * x0 + bs * xT;
+    }
+}
+
+void orc_euler_endpoint(const float* pred, const float* x, float* out, int64_t count, float t)
+{
+    /* sampler.cpp:280-282 */
+    const float bt = t / 1000.0f;
+    for (int64_t i = 0; i < count; i++)
+        out[i] = x[i] - bt * pred[i];
+}

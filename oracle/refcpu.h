@@ -35,6 +35,16 @@
  *                       reshape, the sinusoid and time MLP against a float64
  *                       numpy evaluation, timestep 0 special case, identity
  *                       projections that expose the permutations exactly
+ *   orc_euler_timesteps, orc_make_condition, orc_make_dit_input,
+ *   orc_apply_cfg, orc_euler_step, orc_euler_endpoint, orc_condition_ratio
+ *                       the reference's own known answers (runtime_unit_test
+ *                       CFG 3.0 and endpoint 0.75; sampler_vulkan_runner's
+ *                       condition, 33-channel layout, CFG 2.5/0.4 and step
+ *                       1000->500 cases), float64 closed forms, numpy std
+ *                       with ddof=1, and identities (scale 1 gives pos,
+ *                       rescale 1 matches std(pos), endpoint = step to 0,
+ *                       step to t gives x, the ratio at 1280x720x145 is
+ *                       5t/(1+4t), at 256x256x37 it is t)
  */
 #ifndef SEEDVR2_REFCPU_H
 #define SEEDVR2_REFCPU_H
@@ -191,6 +201,29 @@ typedef struct orc_dit_output {
  * token-major. */
 int orc_dit_output_forward(const orc_dit_output* o, const float* vid, const float* emb, int T, int h, int w,
                            float* out);
+
+/* ---- Euler sampler and latent preparation (src/model/sampler.cpp:27-62,
+ * :181-285; src/core/engine.cpp:79-149).  Latents are flat fp32 arrays in
+ * the reference's [C][T][H][W] order unless a layout is named. */
+
+/* Timesteps of EulerSampler(steps) (sampler.cpp:181-187); returns the count. */
+int orc_euler_timesteps(int steps, float* out);
+/* transformed_condition_timestep(noise_scale, latent) / 1000
+ * (engine.cpp:79-92, :110) for a T x H x W latent. */
+float orc_condition_ratio(float noise_scale, int T, int H, int W);
+/* make_condition_latent (engine.cpp:106-122). */
+void orc_make_condition(const float* encoded, const float* noise, float* out, int64_t count, float ratio);
+/* make_dit_input (engine.cpp:125-149), channel-major, or the token-major
+ * [tokens][33] layout of make_dit_input_vulkan (sampler.cpp:337-357). */
+void orc_make_dit_input(const float* latent, const float* condition, float* out, int64_t tokens, int channel_major);
+/* standard_deviation (sampler.cpp:41-62): double sums in element order. */
+double orc_standard_deviation(const float* x, int64_t count);
+/* EulerSampler::apply_cfg (sampler.cpp:201-236). */
+void orc_apply_cfg(const float* pos, const float* neg, float* out, int64_t count, float scale, float rescale);
+/* EulerSampler::step_to (sampler.cpp:239-265). */
+void orc_euler_step(const float* pred, const float* x, float* out, int64_t count, float t, float t_next);
+/* EulerSampler::endpoint (sampler.cpp:267-285). */
+void orc_euler_endpoint(const float* pred, const float* x, float* out, int64_t count, float t);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,14 @@ EXPORTS = [
     "sv2_dit_workspace_size",
     "sv2_dit_forward",
     "sv2_dit_destroy",
+    "sv2_euler_timesteps",
+    "sv2_condition_ratio",
+    "sv2_make_condition",
+    "sv2_make_dit_input",
+    "sv2_cfg_workspace_size",
+    "sv2_apply_cfg",
+    "sv2_euler_step",
+    "sv2_euler_endpoint",
     "sv2_last_error",
     "sv2_version",
 ]
@@ -277,6 +285,23 @@ def load() -> ctypes.CDLL:
     lib.sv2_dit_forward.restype = i
     lib.sv2_dit_destroy.argtypes = [vp]
     lib.sv2_dit_destroy.restype = None
+    i64 = ctypes.c_int64
+    lib.sv2_euler_timesteps.argtypes = [i, vp]
+    lib.sv2_euler_timesteps.restype = i
+    lib.sv2_condition_ratio.argtypes = [c_f, i, i, i]
+    lib.sv2_condition_ratio.restype = c_f
+    lib.sv2_make_condition.argtypes = [vp, vp, vp, i64, c_f, vp]
+    lib.sv2_make_condition.restype = i
+    lib.sv2_make_dit_input.argtypes = [vp, vp, vp, i64, i, vp]
+    lib.sv2_make_dit_input.restype = i
+    lib.sv2_cfg_workspace_size.argtypes = [i64]
+    lib.sv2_cfg_workspace_size.restype = i64
+    lib.sv2_apply_cfg.argtypes = [vp, vp, vp, i64, c_f, c_f, vp, ctypes.c_size_t, vp]
+    lib.sv2_apply_cfg.restype = i
+    lib.sv2_euler_step.argtypes = [vp, vp, vp, i64, c_f, c_f, vp]
+    lib.sv2_euler_step.restype = i
+    lib.sv2_euler_endpoint.argtypes = [vp, vp, vp, i64, c_f, vp]
+    lib.sv2_euler_endpoint.restype = i
     lib.sv2_last_error.argtypes = []
     lib.sv2_last_error.restype = ctypes.c_char_p
     lib.sv2_version.argtypes = []
@@ -777,3 +802,109 @@ class Dit(_Handle):
         ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
         check(load().sv2_dit_forward(self._h, _ptr(latent), _ptr(text), L, ctypes.c_float(timestep), T, H, W,
                                      _ptr(output), _ptr(workspace), ws_bytes, _stream(stream)), "sv2_dit_forward")
+
+
+def euler_timesteps(steps: int) -> np.ndarray:
+    """EulerSampler(steps).timesteps() (sampler.cpp:181-187), host."""
+    out = np.zeros(max(1, steps), np.float32)
+    n = check(load().sv2_euler_timesteps(steps, out.ctypes.data), "sv2_euler_timesteps")
+    return out[:n]
+
+
+def condition_ratio(noise_scale: float, frames: int, height: int, width: int) -> float:
+    """The noise ratio of make_condition_latent (engine.cpp:79-92, :110)."""
+    return load().sv2_condition_ratio(noise_scale, frames, height, width)
+
+
+def _latent(t, what):
+    import torch
+    if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float32):
+        raise ValueError(f"{what} must be a contiguous fp32 device tensor")
+    return t
+
+
+class EulerSampler:
+    """The Euler v-lerp sampler of the reference (src/model/sampler.h:18-78)
+    on device latents: fp32 contiguous tensors, every update enqueued on the
+    stream with no host synchronisation.  Shape mismatches raise ValueError
+    where the reference returns Status::InvalidArgument."""
+
+    def __init__(self, steps: int):
+        self.timesteps = euler_timesteps(steps)
+        self._ws = {}
+
+    def _workspace(self, device):
+        import torch
+        ws = self._ws.get(device)
+        if ws is None:
+            ws = torch.empty(load().sv2_cfg_workspace_size(0), dtype=torch.uint8, device=device)
+            self._ws[device] = ws
+        return ws
+
+    @staticmethod
+    def _pair(a, b, what):
+        _latent(a, what)
+        _latent(b, what)
+        if a.shape != b.shape:
+            raise ValueError(f"{what}: input shapes differ")
+
+    def apply_cfg(self, positive, negative, scale, rescale, output=None, stream=None):
+        """EulerSampler::apply_cfg (sampler.cpp:201-236)."""
+        import torch
+        self._pair(positive, negative, "apply_cfg")
+        out = torch.empty_like(positive) if output is None else _latent(output, "apply_cfg output")
+        ws = self._workspace(positive.device) if rescale != 0.0 else None
+        check(load().sv2_apply_cfg(_ptr(positive), _ptr(negative), _ptr(out), positive.numel(), scale, rescale,
+                                   _ptr(ws), 0 if ws is None else ws.numel(), _stream(stream)), "sv2_apply_cfg")
+        return out
+
+    def step_to(self, prediction, current, timestep, next_timestep, output=None, stream=None):
+        """EulerSampler::step_to (sampler.cpp:239-265)."""
+        import torch
+        self._pair(prediction, current, "step_to")
+        out = torch.empty_like(current) if output is None else _latent(output, "step_to output")
+        check(load().sv2_euler_step(_ptr(prediction), _ptr(current), _ptr(out), current.numel(), timestep,
+                                    next_timestep, _stream(stream)), "sv2_euler_step")
+        return out
+
+    def endpoint(self, prediction, current, timestep, output=None, stream=None):
+        """EulerSampler::endpoint (sampler.cpp:267-285)."""
+        import torch
+        self._pair(prediction, current, "endpoint")
+        out = torch.empty_like(current) if output is None else _latent(output, "endpoint output")
+        check(load().sv2_euler_endpoint(_ptr(prediction), _ptr(current), _ptr(out), current.numel(), timestep,
+                                        _stream(stream)), "sv2_euler_endpoint")
+        return out
+
+    @staticmethod
+    def make_condition(encoded, noise, ratio, output=None, stream=None):
+        """make_condition_latent (engine.cpp:106-122) with the ratio given, as
+        make_condition_vulkan takes it (sampler.cpp:314-335)."""
+        import torch
+        EulerSampler._pair(encoded, noise, "make_condition")
+        out = torch.empty_like(encoded) if output is None else _latent(output, "make_condition output")
+        check(load().sv2_make_condition(_ptr(encoded), _ptr(noise), _ptr(out), encoded.numel(), ratio,
+                                        _stream(stream)), "sv2_make_condition")
+        return out
+
+    @staticmethod
+    def make_dit_input(latent, condition, channel_major=True, output=None, stream=None):
+        """make_dit_input (engine.cpp:125-149): [16, T, H, W] -> [33, T, H, W];
+        channel_major=False: [tokens, 16] -> [tokens, 33] (sampler.cpp:337-357)."""
+        import torch
+        EulerSampler._pair(latent, condition, "make_dit_input")
+        if channel_major:
+            if latent.dim() < 2 or latent.shape[0] != 16:
+                raise ValueError("make_dit_input: channel-major latents are [16, ...]")
+            shape, tokens = (33,) + tuple(latent.shape[1:]), latent.numel() // 16
+        else:
+            if latent.dim() != 2 or latent.shape[1] != 16:
+                raise ValueError("make_dit_input: token-major latents are [tokens, 16]")
+            shape, tokens = (latent.shape[0], 33), latent.shape[0]
+        out = torch.empty(shape, dtype=torch.float32, device=latent.device) if output is None else output
+        _latent(out, "make_dit_input output")
+        if tuple(out.shape) != shape:
+            raise ValueError(f"make_dit_input: output must be {shape}")
+        check(load().sv2_make_dit_input(_ptr(latent), _ptr(condition), _ptr(out), tokens,
+                                        1 if channel_major else 0, _stream(stream)), "sv2_make_dit_input")
+        return out
