@@ -165,6 +165,15 @@ __device__ inline void store4<F16>(void* base, long long offset, const float v[4
     *reinterpret_cast<f16x4*>(static_cast<_Float16*>(base) + offset) = h;
 }
 
+// Two floats rounded to bf16 (nearest even) in one v_cvt_pk_bf16_f32; a
+// pair converted element by element costs a second conversion and a pack.
+__device__ inline uint32_t bf16_pair_bits(float a, float b)
+{
+    typedef __attribute__((ext_vector_type(2))) float f32x2;
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
 // bf16 rounded to nearest even (identity on attention outputs, which are
 // bf16 values already; the text averages are not).
 template <>
@@ -419,11 +428,7 @@ __device__ inline int vt_offset(int d, int grp)
 // fp16 MFMA: the bf16 values are exact in fp16 within its range.
 __device__ inline f16x2 bf16_pair_as_f16(float a, float b)
 {
-    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-    bf16x2 r;
-    r[0] = static_cast<__bf16>(a);
-    r[1] = static_cast<__bf16>(b);
-    const uint32_t u = __builtin_bit_cast(uint32_t, r);
+    const uint32_t u = bf16_pair_bits(a, b);
     return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, u << 16),
                                                                 __builtin_bit_cast(float, u & 0xffff0000u)));
 }
@@ -1128,7 +1133,6 @@ __device__ inline void store_rounded(int out_dtype, void* base, long long offset
 __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const WindowBox& box, int wi, int head,
                                      int qrow, int g, const f32x16 o[4], float inv_l)
 {
-    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
     const long long q_col = static_cast<long long>(head) * kHeadDim;
     const bool text = qrow >= box.vlen;
     long long out_off;
@@ -1150,15 +1154,9 @@ __device__ inline void write_outputs(const AttnParams& p, const Staged& s, const
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 pre[e] = o[dt][4 * rq + e] * inv_l;
-            bf16x2 a;
-            bf16x2 b;
-            a[0] = static_cast<__bf16>(pre[0]);
-            a[1] = static_cast<__bf16>(pre[1]);
-            b[0] = static_cast<__bf16>(pre[2]);
-            b[1] = static_cast<__bf16>(pre[3]);
             if (p.dbg_pre)
                 store4<F32>(p.dbg_pre, pre_row + d, pre);
-            store_rounded(dt_out, dst, out_off + d, __builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+            store_rounded(dt_out, dst, out_off + d, bf16_pair_bits(pre[0], pre[1]), bf16_pair_bits(pre[2], pre[3]));
         }
 }
 
@@ -1175,7 +1173,6 @@ __device__ inline void write_outputs_lds(const AttnParams& p, const Staged& s, c
                                          int head, int q_wave0, int q_end, int lane, const f32x16 o[4],
                                          float inv_l, char* stage)
 {
-    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
     const int lr = lane & 31;
     const int g = lane >> 5;
     const int qrow = q_wave0 + lr;
@@ -1197,14 +1194,8 @@ __device__ inline void write_outputs_lds(const AttnParams& p, const Staged& s, c
                 pre[e] = o[dt][4 * rq + e] * inv_l;
             if (p.dbg_pre && qrow < q_end)
                 store4<F32>(p.dbg_pre, pre_row + d, pre);
-            bf16x2 a;
-            bf16x2 b;
-            a[0] = static_cast<__bf16>(pre[0]);
-            a[1] = static_cast<__bf16>(pre[1]);
-            b[0] = static_cast<__bf16>(pre[2]);
-            b[1] = static_cast<__bf16>(pre[3]);
-            uint32_t lo = __builtin_bit_cast(uint32_t, a);
-            uint32_t hi = __builtin_bit_cast(uint32_t, b);
+            uint32_t lo = bf16_pair_bits(pre[0], pre[1]);
+            uint32_t hi = bf16_pair_bits(pre[2], pre[3]);
             if (f16_out)
             {
                 // the bf16 values are exact in fp16 within its range
