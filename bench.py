@@ -141,15 +141,15 @@ def dit_bench(dev, steps: int, warmup: int):
             wbytes[0] += out[f].numel() * out[f].element_size()
         return out
 
-    blocks = []
+    weights, cfgs = [], []
     for i in range(DIT_BLOCKS):
         shared, last, shifted = block_flags(i, DIT_BLOCKS)
         w = {"vid": branch(), "freqs": reference_freqs()}
         if not shared:
             w["txt"] = branch()
-        cfg = sv2hip.block_config(block_index=i, shared_weights=int(shared), last_layer=int(last),
-                                  shifted_window=int(shifted), window_t=WIN[0], window_h=WIN[1], window_w=WIN[2])
-        blocks.append(sv2hip.DitBlock.from_device(cfg, w, sv2hip.F16))
+        weights.append(w)
+        cfgs.append(dict(block_index=i, shared_weights=int(shared), last_layer=int(last), shifted_window=int(shifted),
+                         window_t=WIN[0], window_h=WIN[1], window_w=WIN[2]))
     f16, f32 = torch.float16, torch.float32
     wi = {"w_vid": randn((D, 4 * LATENT_C), f16), "b_vid": randn((D,), f32),
           "w_txt": randn((D, TEXT_C), f16), "b_txt": randn((D,), f32),
@@ -161,26 +161,39 @@ def dit_bench(dev, steps: int, warmup: int):
           "w_proj": randn((4 * OUT_C, D), f16), "b_proj": randn((4 * OUT_C,), f32)}
     inp = sv2hip.DitInput.create(wi, sv2hip.F16, on_device=True)
     outp = sv2hip.DitOutput.create(wo, sv2hip.F16, on_device=True)
-    dit = sv2hip.Dit.create(inp, blocks, outp)
     latent = torch.randn((LATENT_C, T, 2 * H, 2 * W), generator=g, device=dev)
     latent[LATENT_C - 1].fill_(1.0)
     text = torch.randn((L_TXT, TEXT_C), generator=g, device=dev)
     out = torch.empty((OUT_C, T, 2 * H, 2 * W), device=dev)
-    ws = torch.empty(dit.workspace_size(T, 2 * H, 2 * W, L_TXT), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for a, b in ev:
-        a.record(stream)
-        dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
-        b.record(stream)
-    torch.cuda.synchronize()
-    ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    finite = bool(torch.isfinite(out).all().item())
+
+    def timed(fused: bool):
+        # the blocks borrow the same device weights; fused selects the
+        # hand-written MFMA InnerProducts with their passes fused in
+        blocks = [sv2hip.DitBlock.from_device(sv2hip.block_config(fused_gemm=int(fused), **c), w, sv2hip.F16)
+                  for c, w in zip(cfgs, weights)]
+        dit = sv2hip.Dit.create(inp, blocks, outp)
+        ws = torch.empty(dit.workspace_size(T, 2 * H, 2 * W, L_TXT), dtype=torch.uint8, device=dev)
+        for _ in range(warmup):
+            dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in ev:
+            a.record(stream)
+            dit.forward(latent, text, 1000.0, out, workspace=ws, stream=stream)
+            b.record(stream)
+        torch.cuda.synchronize()
+        t = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+        ok = bool(torch.isfinite(out).all().item())
+        dit.close()
+        for blk in blocks:
+            blk.close()
+        del ws
+        return t, ok
+
+    ms, finite = timed(False)
+    ms_fused, finite_fused = timed(True)
     gemm_f, attn_f = dit_flops()
-    dit.close()
     return {
         "ms": round(ms, 3),
         "steps": steps,
@@ -191,6 +204,8 @@ def dit_bench(dev, steps: int, warmup: int):
         "attention_tflop": round(attn_f / 1e12, 2),
         "block_weights_gb": round(wbytes[0] / 1e9, 2),
         "output_finite": finite,
+        "fused_inner_products_ms": round(ms_fused, 3),
+        "fused_inner_products_finite": finite_fused,
         "workload": ("SeedVR2-3B DiT forward, 1280x720x21 (latent 33x6x90x160 -> grid 6x45x80), 32 blocks, "
                      "hidden 2560, 20 heads, MLP 6912 SwiGLU, 58 text tokens, windows 2x9x16 alternating "
                      "unshifted / shifted, fp16 weights and activations, fp32 accumulation"),

@@ -206,6 +206,12 @@ typedef struct sv2_block_config {
     int window_w;        /* param 11 */
     int rope_mode;       /* param 12: sv2_rope_mode (default SV2_ROPE_REFERENCE) */
     int qk_norm;         /* param 13: 1 (default) = per-head RMSNorm * gamma on q, k */
+    int fused_gemm;      /* param 14: 1 = the video branch's InnerProducts on the hand-written
+                            MFMA kernel with their passes fused (sv2_inner_product_f16: qkv;
+                            proj_out + gated residual; gate/in + SwiGLU; out + gated residual),
+                            fp16 compute only (ignored for fp32) and not while debug captures
+                            are set; needs dim % 256 == 0 and mlp_hidden % 128 == 0.
+                            0 (default) = library GEMMs and separate passes. */
 } sv2_block_config;
 
 /* Weights of one branch ("vid", "txt" or the shared "all"), in the order the
@@ -407,6 +413,29 @@ int64_t sv2_dit_workspace_size(sv2_dit* dit, int frames, int height, int width, 
 int sv2_dit_forward(sv2_dit* dit, const float* latent, const float* text, int text_len, float timestep, int frames,
                     int height, int width, float* output, void* workspace, size_t workspace_bytes, void* stream);
 void sv2_dit_destroy(sv2_dit* dit);
+
+/* ---- fp16 InnerProduct with the pass that follows it fused in, on a
+ * hand-written gfx950 MFMA kernel.  Replaces the block's ncnn InnerProduct
+ * layers (load_inner_product, seedvr2_dit_block.cpp:27-55; the five per
+ * branch, :668-674) together with the elementwise pass after each:
+ *   SV2_EPI_STORE     y [rows, out] = fp16(x W^T)                      (qkv)
+ *   SV2_EPI_RESIDUAL  y [rows, out] = fp16((fp16(x W^T) + bias) * gate
+ *                     + residual), bias and gate optional (NULL): the
+ *                     gated residual after proj_out and mlp_out_proj
+ *                     (apply_ada_output_and_residual, :807-825)
+ *   SV2_EPI_SWIGLU    y [rows, out] = fp16(silu(g) * u), g = fp16(x W^T),
+ *                     u = fp16(x W_value^T): mlp_gate_proj, mlp_in_proj and
+ *                     the gate of apply_mlp (:1093-1112)
+ * x fp16 [rows, in]; W, W_value fp16 [out, in] row-major (the InnerProduct
+ * weight layout); residual fp16 [rows, out]; bias, gate fp32 [out].  Every
+ * fp32 step follows the unfused kernels' order.  Requires in % 64 == 0 and
+ * out % 256 == 0 (SV2_EPI_SWIGLU: out % 128 == 0); SV2_EUNSUPPORTED
+ * otherwise.  y may not alias x, W or residual. */
+#define SV2_EPI_STORE 0
+#define SV2_EPI_RESIDUAL 1
+#define SV2_EPI_SWIGLU 2
+int sv2_inner_product_f16(const void* x, const void* w, const void* w_value, void* y, int rows, int in, int out,
+                          int epilogue, const float* bias, const float* gate, const void* residual, void* stream);
 
 /* ---- Euler sampler (src/model/sampler.h:18-78) and the latent preparation
  * of the engine loop (src/core/engine.cpp:79-149, :306-350).  Latents are

@@ -11,7 +11,11 @@
 #include "ncnn_format.h"
 #include "sv2_internal.h"
 
+using sv2::gemm_mfma;
 using sv2::gemm_rows;
+using sv2::kGemmResidual;
+using sv2::kGemmStore;
+using sv2::kGemmSwiGLU;
 
 namespace
 {
@@ -83,6 +87,11 @@ int validate_config(const sv2_block_config& c)
         return sv2::set_error(SV2_EINVAL, "block: window extents must be >= 0");
     if (c.rope_mode < SV2_ROPE_REFERENCE || c.rope_mode > SV2_ROPE_NONE)
         return sv2::set_error(SV2_EINVAL, "block: unknown rope mode");
+    if (c.fused_gemm && (!sv2::gemm_mfma_supported(c.dim, 3 * c.dim, sv2::kGemmStore) ||
+                         !sv2::gemm_mfma_supported(c.dim, c.mlp_hidden, sv2::kGemmSwiGLU) ||
+                         !sv2::gemm_mfma_supported(c.mlp_hidden, c.dim, sv2::kGemmResidual)))
+        return sv2::set_error(SV2_EUNSUPPORTED,
+                              "block: fused InnerProducts need dim % 256 == 0 and mlp_hidden % 128 == 0");
     return SV2_OK;
 }
 
@@ -290,7 +299,7 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
 // (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).  `table` is the
 // branch's MLP modulation table.
 int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, const float* table, const void* x,
-               int rows, void* out, char* m, char* g, char* u)
+               int rows, void* out, char* m, char* g, char* u, bool fused)
 {
     using namespace sv2;
     if (rows == 0)
@@ -300,6 +309,15 @@ int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, cons
     if ((rc = launch_rmsnorm_table(x, m, dt, rows, D, b->cfg.norm_eps, table, br.ada[3], nullptr, 1, stream)) !=
         SV2_OK)
         return rc;
+    if (fused)
+    {
+        // gate/in products with the SwiGLU gate, then the out product with
+        // the gated residual (mlp_gate is the table's third row)
+        if ((rc = gemm_mfma(stream, rows, D, F, m, br.w_gate, br.w_in, g, kGemmSwiGLU, nullptr, nullptr,
+                            nullptr)) != SV2_OK)
+            return rc;
+        return gemm_mfma(stream, rows, F, D, g, br.w_out, nullptr, out, kGemmResidual, nullptr, table + 2 * D, x);
+    }
     if ((rc = gemm_rows(stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
         (rc = gemm_rows(stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
         return rc;
@@ -356,6 +374,7 @@ void sv2_block_config_default(sv2_block_config* c)
     c->norm_eps = 1e-5f;
     c->rope_mode = SV2_ROPE_REFERENCE;
     c->qk_norm = 1;
+    c->fused_gemm = 0;
 }
 
 int sv2_block_create(const sv2_block_config* config, const sv2_block_branch* vid, const sv2_block_branch* txt,
@@ -425,6 +444,7 @@ int sv2_block_load(const char* param_path, const char* bin_path, int compute_dty
     c.window_w = layer->get_int(11, 0);
     c.rope_mode = layer->get_int(12, SV2_ROPE_REFERENCE);
     c.qk_norm = layer->get_int(13, 1) != 0;
+    c.fused_gemm = layer->get_int(14, 0) != 0;
     int rc = validate_config(c);
     if (rc != SV2_OK)
         return rc;
@@ -587,9 +607,14 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
     if ((rc = launch_rmsnorm_table(vid, xa, dt, Lv, D, c.norm_eps, tab_va, vb.ada[0], nullptr, 1, stream)) != SV2_OK)
         return rc;
-    if ((rc = gemm_rows(stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
-        return rc;
     const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
+    // the video branch on the fused MFMA InnerProducts (param 14); the text
+    // rows (a few dozen) stay on the library GEMMs
+    const bool fused = c.fused_gemm && dt == SV2_F16 && !dbg;
+    if ((rc = fused ? gemm_mfma(stream, Lv, D, 3 * D, xa, vb.w_qkv, nullptr, qkv_v, kGemmStore, nullptr, nullptr,
+                                nullptr)
+                    : gemm_rows(stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
+        return rc;
     auto capture = [&](float* dst, const void* src, int rows, int cols) {
         return dst ? launch_to_f32(dst, src, dt, static_cast<long long>(rows) * cols, stream) : SV2_OK;
     };
@@ -626,12 +651,21 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                 (Lt > 0 && (rc = capture(dbg->attention_txt, att_t, Lt, D)) != SV2_OK)))
         return rc;
     // output projections; their bias is added in the gated residual (:1180-1209)
-    if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
-        return rc;
-    if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
-        return rc;
-    if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
-        return rc;
+    if (fused)
+    {
+        if ((rc = gemm_mfma(stream, Lv, D, D, att_v, vb.w_proj, nullptr, p_v, kGemmResidual, vb.b_proj,
+                            tab_va + 2 * D, vid)) != SV2_OK)
+            return rc;
+    }
+    else
+    {
+        if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
+            return rc;
+        if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
+            return rc;
+        if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
+            return rc;
+    }
     if (Lt > 0)
     {
         if ((rc = gemm_rows(stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK)
@@ -644,7 +678,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
             return rc;
     }
     // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)
-    if ((rc = branch_mlp(b, stream, vb, tab_vm, p_v, Lv, vid_out, xa, g, u)) != SV2_OK)
+    if ((rc = branch_mlp(b, stream, vb, tab_vm, p_v, Lv, vid_out, xa, g, u, fused)) != SV2_OK)
         return rc;
     if (Lt > 0)
     {
@@ -657,7 +691,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
             if ((rc = launch_residual_table(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 2, stream)) != SV2_OK)
                 return rc;
         }
-        else if ((rc = branch_mlp(b, stream, tb, tab_tm, p_t, Lt, txt_out, xa, g, u)) != SV2_OK)
+        else if ((rc = branch_mlp(b, stream, tb, tab_tm, p_t, Lt, txt_out, xa, g, u, false)) != SV2_OK)
         {
             return rc;
         }

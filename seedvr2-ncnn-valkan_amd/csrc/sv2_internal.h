@@ -133,6 +133,18 @@ int launch_residual_table(void* x, const void* residual, int dtype, int rows, in
 // fp32 on rocBLAS.
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y);
 
+// fp16 y = epilogue(x W^T) on the hand-written MFMA kernel (gemm.hip), x
+// [rows][in], W (and w2) [out][in].  Epilogues: store; the gated residual
+// y = fp16((fp16(x W^T) + bias) * gate + residual) (bias, gate optional);
+// SwiGLU y = silu(fp16(x W^T)) * fp16(x W2^T).  Needs in % 64 == 0 and
+// out % 256 == 0 (SwiGLU: out % 128 == 0).
+constexpr int kGemmStore = 0;
+constexpr int kGemmResidual = 1;
+constexpr int kGemmSwiGLU = 2;
+bool gemm_mfma_supported(int in, int out, int epi);
+int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, const void* w2, void* y,
+              int epi, const float* bias, const float* gate, const void* residual);
+
 // Allocates device memory for `count` host fp32 values, stores them as dtype
 // (SV2_F32 or SV2_F16, round to nearest) and records the allocation in *owned.
 int upload_weights(std::vector<void*>* owned, const float* host, size_t count, int dtype, const void** dev);

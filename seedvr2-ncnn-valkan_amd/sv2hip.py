@@ -63,6 +63,7 @@ EXPORTS = [
     "sv2_dit_workspace_size",
     "sv2_dit_forward",
     "sv2_dit_destroy",
+    "sv2_inner_product_f16",
     "sv2_euler_timesteps",
     "sv2_condition_ratio",
     "sv2_make_condition",
@@ -135,6 +136,7 @@ class BlockConfig(ctypes.Structure):
         ("window_w", ctypes.c_int),
         ("rope_mode", ctypes.c_int),
         ("qk_norm", ctypes.c_int),
+        ("fused_gemm", ctypes.c_int),
     ]
 
 
@@ -285,6 +287,8 @@ def load() -> ctypes.CDLL:
     lib.sv2_dit_forward.restype = i
     lib.sv2_dit_destroy.argtypes = [vp]
     lib.sv2_dit_destroy.restype = None
+    lib.sv2_inner_product_f16.argtypes = [vp, vp, vp, vp, i, i, i, i, vp, vp, vp, vp]
+    lib.sv2_inner_product_f16.restype = i
     i64 = ctypes.c_int64
     lib.sv2_euler_timesteps.argtypes = [i, vp]
     lib.sv2_euler_timesteps.restype = i
@@ -908,3 +912,29 @@ class EulerSampler:
         check(load().sv2_make_dit_input(_ptr(latent), _ptr(condition), _ptr(out), tokens,
                                         1 if channel_major else 0, _stream(stream)), "sv2_make_dit_input")
         return out
+
+
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
+
+
+def inner_product_f16(x, w, y, epilogue=EPI_STORE, w_value=None, bias=None, gate=None, residual=None,
+                      stream=None):
+    """y = epilogue(x W^T) on the MFMA kernel (sv2_inner_product_f16): x fp16
+    [rows, in], w (and w_value) fp16 [out, in], y fp16 [rows, out]; bias and
+    gate fp32 [out], residual fp16 [rows, out] (device tensors)."""
+    import torch
+    rows, k = x.shape
+    out = w.shape[0]
+    for name, t, shape in (("x", x, (rows, k)), ("w", w, (out, k)), ("y", y, (rows, out))):
+        if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float16 and tuple(t.shape) == shape):
+            raise ValueError(f"{name} must be a contiguous fp16 device tensor {shape}")
+    for name, t, dt, shape in (("w_value", w_value, torch.float16, (out, k)), ("bias", bias, torch.float32, (out,)),
+                               ("gate", gate, torch.float32, (out,)),
+                               ("residual", residual, torch.float16, (rows, out))):
+        if t is not None and not (t.is_cuda and t.is_contiguous() and t.dtype == dt and tuple(t.shape) == shape):
+            raise ValueError(f"{name} must be a contiguous {dt} device tensor {shape}")
+    check(load().sv2_inner_product_f16(_ptr(x), _ptr(w), _ptr(w_value), _ptr(y), rows, k, out, epilogue,
+                                       _ptr(bias), _ptr(gate), _ptr(residual), _stream(stream)),
+          "sv2_inner_product_f16")
+    return y
+

@@ -1,0 +1,135 @@
+"""GPU parity of the fp16 InnerProduct MFMA kernel (sv2_inner_product_f16,
+csrc/gemm.hip), which replaces the block's ncnn InnerProducts
+(seedvr2_dit_block.cpp:27-55, :668-674) and fuses the pass after each:
+  * plain products against the float64 product of the same fp16 inputs (on
+    the CPU, over a sample of rows) rounded to fp16: every element within one
+    fp16 ulp of the larger of the two values plus the fp32 accumulation
+    allowance 2^-20 * sum_k |x_k w_k| (outputs near zero cancel, and their
+    fp32 rounding error is many fp16 ulps of the tiny result; a sequential
+    fp32 sum shows the same), and the mean difference far below an ulp;
+  * the gated-residual and SwiGLU epilogues against the unfused arithmetic
+    (ada_residual / swiglu kernels, seedvr2_dit_block.cpp:807-825,
+    :1093-1112) applied in float32 on the host to the kernel's own stored
+    products: the residual bit for bit, SwiGLU within one fp16 ulp (the
+    host's exp is not the device's);
+shapes: the DiT block's products at 720p x 21 frames (21600 rows;
+2560 -> 7680, 2560 -> 2560, 2560 -> 2 x 6912, 6912 -> 2560), rows that are
+not a multiple of the 256-row tile, one row, and the unsupported shapes'
+error codes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp16(x):
+    x = np.abs(np.asarray(x, np.float32)).astype(np.float16)
+    return np.spacing(np.maximum(x, np.float16(6.1e-5))).astype(np.float32)
+
+
+def rand16(shape, scale, gen):
+    return (torch.randn(shape, generator=gen, device="cuda") * scale).to(torch.float16)
+
+
+def sample_rows(rows, count=192):
+    """The first and last rows, the rows around each 256-row tile edge near
+    the end, and a seeded random sample."""
+    rng = np.random.default_rng(rows)
+    idx = {0, rows - 1, max(0, rows - 257), max(0, rows - 256)}
+    idx.update(rng.integers(0, rows, size=min(rows, count)).tolist())
+    return np.array(sorted(idx))
+
+
+def reference64(x, w, idx):
+    """float64 product of the fp16 inputs for rows idx rounded to fp16, and
+    the fp32 accumulation allowance 2^-20 * sum_k |x_k w_k|."""
+    xs = x[torch.from_numpy(idx).cuda()].double().cpu().numpy()
+    wd = w.double().cpu().numpy().T
+    return (xs @ wd).astype(np.float16), (np.abs(xs) @ np.abs(wd)) * 2.0 ** -20
+
+
+def assert_ulp(got, ref, ulps=1.0, slack=0.0):
+    g = np.asarray(got, np.float32)
+    r = np.asarray(ref, np.float32)
+    d = np.abs(g - r)
+    bad = d > ulps * ulp16(np.maximum(np.abs(g), np.abs(r))) + slack
+    assert not bad.any(), f"{int(bad.sum())} of {d.size} beyond {ulps} ulp, max {d.max():.3e}"
+    return float(d.mean())
+
+
+@pytest.mark.parametrize("rows,k,n", [(21600, 2560, 7680), (21600, 6912, 2560), (300, 64, 256), (1, 2560, 512),
+                                      (513, 2560, 2560)])
+def test_store(hip, rows, k, n):
+    gen = torch.Generator(device="cuda").manual_seed(rows + k + n)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    hip.inner_product_f16(x, w, y)
+    torch.cuda.synchronize()
+    idx = sample_rows(rows)
+    got = y.cpu().numpy()[idx]
+    ref, slack = reference64(x, w, idx)
+    mean = assert_ulp(got, ref, slack=slack)
+    assert mean < 2e-4
+
+
+@pytest.mark.parametrize("rows", [21600, 777])
+@pytest.mark.parametrize("bias,gate", [(True, True), (False, True), (True, False)])
+def test_residual(hip, rows, bias, gate):
+    k, n = 2560, 2560
+    gen = torch.Generator(device="cuda").manual_seed(rows + 7)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    r = rand16((rows, n), 1.0, gen)
+    b = torch.randn(n, generator=gen, device="cuda") * 0.1 if bias else None
+    g = torch.randn(n, generator=gen, device="cuda") if gate else None
+    p = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    y = torch.empty_like(p)
+    hip.inner_product_f16(x, w, p)
+    hip.inner_product_f16(x, w, y, hip.EPI_RESIDUAL, bias=b, gate=g, residual=r)
+    torch.cuda.synchronize()
+    v = p.float().cpu().numpy()
+    if bias:
+        v = v + b.cpu().numpy()[None, :]
+    if gate:
+        v = v * g.cpu().numpy()[None, :]
+    v = v + r.float().cpu().numpy()
+    assert np.array_equal(y.cpu().numpy(), v.astype(np.float16))
+
+
+@pytest.mark.parametrize("rows,k,f", [(21600, 2560, 6912), (300, 64, 256)])
+def test_swiglu(hip, rows, k, f):
+    gen = torch.Generator(device="cuda").manual_seed(rows + f)
+    x = rand16((rows, k), 1.0, gen)
+    wg = rand16((f, k), 0.02, gen)
+    wu = rand16((f, k), 0.02, gen)
+    pg = torch.empty((rows, f), dtype=torch.float16, device="cuda")
+    pu = torch.empty_like(pg)
+    y = torch.empty_like(pg)
+    hip.inner_product_f16(x, wg, pg)
+    hip.inner_product_f16(x, wu, pu)
+    hip.inner_product_f16(x, wg, y, hip.EPI_SWIGLU, w_value=wu)
+    torch.cuda.synchronize()
+    gg = pg.float().cpu().numpy()
+    uu = pu.float().cpu().numpy()
+    ref = ((gg / (np.float32(1.0) + np.exp(-gg))) * uu).astype(np.float16)
+    assert_ulp(y.float().cpu().numpy(), ref)
+
+
+def test_unsupported_shapes(hip):
+    x = torch.zeros((4, 48), dtype=torch.float16, device="cuda")
+    w = torch.zeros((256, 48), dtype=torch.float16, device="cuda")
+    y = torch.zeros((4, 256), dtype=torch.float16, device="cuda")
+    with pytest.raises(hip.Sv2Error) as e:
+        hip.inner_product_f16(x, w, y)  # in not a multiple of 64
+    assert e.value.code == hip.SV2_EUNSUPPORTED
+    x = torch.zeros((4, 64), dtype=torch.float16, device="cuda")
+    w = torch.zeros((200, 64), dtype=torch.float16, device="cuda")
+    y = torch.zeros((4, 200), dtype=torch.float16, device="cuda")
+    with pytest.raises(hip.Sv2Error) as e:
+        hip.inner_product_f16(x, w, y)  # out not a multiple of 256
+    assert e.value.code == hip.SV2_EUNSUPPORTED
