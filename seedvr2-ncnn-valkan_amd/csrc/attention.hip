@@ -612,21 +612,40 @@ __device__ inline void query_finish(const AttnParams& p, const Staged& s, const 
     }
     if (!is_video)
         return;
+    // RoPE lookups: the lane's three table rows (t, y, x of its token) are
+    // resolved once; the axis and slot of each pair are constants of the
+    // unrolled chunk and pair indices for either value of the lane half g, so
+    // a lookup is a select between two precomputed offsets
     const uint32_t packed = static_cast<uint32_t>(s.rows[qrow].y);
     const RopeBase rb = rope_base(box);
+    const int base0 = (rb.b[0] + static_cast<int>(packed & 1023u)) * kRopePairSlots;
+    const int base1 = (rb.b[1] + static_cast<int>((packed >> 10) & 1023u)) * kRopePairSlots;
+    const int base2 = (rb.b[2] + static_cast<int>((packed >> 20) & 1023u)) * kRopePairSlots;
 #pragma unroll
     for (int c = 0; c < 8; c++)
     {
         const int d0 = 16 * c + 8 * g;
         scale_rotate8<RM != SV2_ROPE_NONE>(&x[8 * c], &s.gamma[d0], inv, p.qk_norm != 0, [&](int q) {
-            int axis, slot;
-            rope_axis_slot<RM>(d0 + 2 * q, &axis, &slot);
-            const int local = static_cast<int>((packed >> (10 * axis)) & 1023u);
-            const int row0 = axis == 0 ? rb.b[0] : (axis == 1 ? rb.b[1] : rb.b[2]);
-            return s.rope[(row0 + local) * kRopePairSlots + slot];
+            int axis_a, slot_a, axis_b, slot_b;
+            rope_axis_slot<RM>(16 * c + 2 * q, &axis_a, &slot_a);
+            rope_axis_slot<RM>(16 * c + 2 * q + 8, &axis_b, &slot_b);
+            const int ia = (axis_a == 0 ? base0 : (axis_a == 1 ? base1 : base2)) + slot_a;
+            const int ib = (axis_b == 0 ? base0 : (axis_b == 1 ? base1 : base2)) + slot_b;
+            return s.rope[g ? ib : ia];
         });
         qf[c] = __builtin_bit_cast(bf16x8, to_bf16x8(&x[8 * c]));
     }
+}
+
+// Makes the query operand's loads complete here rather than at its first use
+// in the tile loop: the compiler's wait for them counts only its own memory
+// operations (not the key/value fetches, issued through inline assembly), so
+// a wait inside the loop would also hold the fetches in flight there.
+__device__ inline void settle(bf16x8 qf[8])
+{
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+        asm volatile("" : "+v"(qf[c]));
 }
 
 // Per-thread RoPE lookup of a key chunk: the chunk (8 dims) is fixed per
@@ -1240,7 +1259,8 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform: wave-derived offsets live in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool loader = tid < kLoaderThreads;
 
     // XCD-aware decode: workgroup ids go round-robin over the 8 XCDs; the query
@@ -1290,6 +1310,7 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     query_load<TI>(p, s, box, head, qrow_c, g, qraw);
     bf16x8 qf[8];
     query_finish<TI, RM>(p, s, box, qrow_c, g, qraw, qf);
+    settle(qf);
 
     f32x16 o[4];
 #pragma unroll
