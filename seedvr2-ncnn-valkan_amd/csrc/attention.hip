@@ -62,6 +62,7 @@ constexpr int kTextPad = 64;                 // text rows of the prepared worksp
 constexpr int kMaxVideoRows = 4096;          // video tokens per window (local coordinates fit 10 bits)
 constexpr int kPrepRows = 16;                // text rows per text_prepare workgroup
 constexpr int kMaxLds = 160 * 1024;          // LDS of one gfx950 CU
+constexpr int kMaxOrdered = 256;             // plans with at most this many windows run largest-first
 // s_waitcnt immediates for vmcnt(0) / vmcnt(4) with expcnt and lgkmcnt left
 // unconstrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
 // vmcnt[5:4] << 14).
@@ -269,6 +270,8 @@ struct AttnParams
     uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_vt;       // [heads][128][text_pad] fp16, prepared and transposed
+    int ordered;            // windows dispatched in the order of `order` (else in plan order)
+    int16_t order[kMaxOrdered]; // window indices by decreasing video length
 };
 
 // ---------------------------------------------------------------- lane helpers
@@ -1274,8 +1277,10 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     const int qb = slot - grp * p.nqb;
     if (pair >= p.npairs)
         return;
-    const int wi = pair / p.heads;
-    const int head = pair - wi * p.heads;
+    // largest windows first, so the last workgroups of the launch are short
+    const int wslot = pair / p.heads;
+    const int head = pair - wslot * p.heads;
+    const int wi = p.ordered ? static_cast<int>(p.order[wslot]) : wslot;
     const WindowBox box = window_box(p.plan, wi);
     Geometry gm;
     gm.vlen = box.vlen;
@@ -1650,6 +1655,22 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
     }
     if (a->rope_mode == SV2_ROPE_NONE)
         rope_rows = 0;
+    // dispatch order: windows by decreasing video length (stable), so that a
+    // plan's ragged small windows form the tail of the launch
+    p->ordered = p->plan.nwin <= kMaxOrdered ? 1 : 0;
+    if (p->ordered)
+    {
+        int idx[kMaxOrdered];
+        int len[kMaxOrdered];
+        for (int wi = 0; wi < p->plan.nwin; wi++)
+        {
+            idx[wi] = wi;
+            len[wi] = window_box(p->plan, wi).vlen;
+        }
+        std::stable_sort(idx, idx + p->plan.nwin, [&](int x, int y) { return len[x] > len[y]; });
+        for (int wi = 0; wi < p->plan.nwin; wi++)
+            p->order[wi] = static_cast<int16_t>(idx[wi]);
+    }
     const int64_t qkv_elems = static_cast<int64_t>(a->rule.frames) * a->rule.height * a->rule.width * 3 * a->heads * kHeadDim;
     if (qkv_elems >= (int64_t(1) << 40))
         return set_error(SV2_EUNSUPPORTED, "attention: qkv tensor too large");
