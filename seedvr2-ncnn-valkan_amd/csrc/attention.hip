@@ -1346,8 +1346,18 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
         // (fetched one step earlier)
         const int ln = opaque(lane);
         const bool fetch = kb + 2 <= last_tile;
+        const bool value_wave = wave >= 8;
         if constexpr (TI::kDma)
         {
+            // the value waves prepare tile kb+1 before they attend, while the
+            // key waves attend first: one group's VALU work meets the other's
+            // MFMAs.  Tile kb+1 has landed once nothing is outstanding (its
+            // fetches are the value waves' only ones in flight here).
+            if (value_wave && kb + 1 < gm.nkb)
+            {
+                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+                prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+            }
             if (fetch)
                 dma_tile<TI>(p, gm, s, smem, head, kb + 2, wave, ln);
         }
@@ -1364,10 +1374,13 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
         {
             if constexpr (TI::kDma)
             {
-                // tile kb+1 has landed once only tile kb+2's fetches (if any)
-                // are outstanding
-                wait_tile_fetch(wave, fetch);
-                prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+                // key waves: tile kb+1 has landed once only tile kb+2's
+                // fetches (if any) are outstanding
+                if (!value_wave)
+                {
+                    wait_tile_fetch(wave, fetch);
+                    prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+                }
             }
             else if (loader)
             {
