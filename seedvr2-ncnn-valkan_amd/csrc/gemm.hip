@@ -122,30 +122,53 @@ __device__ inline float h2f(_Float16 v)
     return static_cast<float>(v);
 }
 
+// Per-column epilogue operands of a lane's 8 output columns (the same for
+// every row the lane stores): bias and gate, read once.
+struct EpiCols
+{
+    float b[8];
+    float g[8];
+};
+
+__device__ inline EpiCols epi_cols(const GemmArgs& a, int col)
+{
+    EpiCols c;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+    {
+        c.b[e] = 0.f;
+        c.g[e] = 1.f;
+    }
+    if (a.epi == kResidual)
+    {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            if (a.bias)
+                c.b[e] = a.bias[col + e];
+            if (a.gate)
+                c.g[e] = a.gate[col + e];
+        }
+    }
+    return c;
+}
+
 // Epilogue of one 16-byte segment (8 columns) of an output row.
-__device__ inline h8 finish_segment(const GemmArgs& a, const h8 p, long long row, int col)
+__device__ inline h8 finish_segment(const GemmArgs& a, const EpiCols& c, const h8 p, long long row, int col)
 {
     h8 out;
     if (a.epi == kStore)
         return p;
     // kResidual
-    float b[8];
-    float g[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-    {
-        b[e] = a.bias ? a.bias[col + e] : 0.f;
-        g[e] = a.gate ? a.gate[col + e] : 1.f;
-    }
     const h8 res = *reinterpret_cast<const h8*>(a.r + row * a.n + col);
 #pragma unroll
     for (int e = 0; e < 8; e++)
     {
         float v = h2f(p[e]);
         if (a.bias)
-            v = v + b[e];
+            v = v + c.b[e];
         if (a.gate)
-            v = v * g[e];
+            v = v * c.g[e];
         v = v + h2f(res[e]);
         out[e] = static_cast<_Float16>(v);
     }
@@ -312,6 +335,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
     __builtin_amdgcn_wave_barrier();
     const int chunk = lane & 7;
     const int col = n0 + 64 * wn + 8 * chunk;
+    const EpiCols ec = epi_cols(a, col);
 #pragma unroll 4
     for (int it = 0; it < 16; it++)
     {
@@ -320,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
         if (row >= a.m)
             continue;
         const h8 p = *reinterpret_cast<const h8*>(mine + rl * kEpiStride + chunk * 16);
-        *reinterpret_cast<h8*>(a.y + row * a.n + col) = finish_segment(a, p, row, col);
+        *reinterpret_cast<h8*>(a.y + row * a.n + col) = finish_segment(a, ec, p, row, col);
     }
 }
 
