@@ -218,7 +218,12 @@ def sampler_bench(dev, reps: int = 50):
     predictions, and the Euler update; per operation the mean time over
     `reps` launches and its algorithmic HBM bytes (each element read and
     written once per pass: DiT input 65 x 4 B per token, CFG 12 B + the
-    rescale pass 8 B per element, Euler 12 B per element)."""
+    rescale pass 8 B per element, Euler 12 B per element).
+
+    The `reps` launches of an operation are captured in one HIP graph and
+    the replay is timed, so "us" is the device time of its kernels; an eager
+    loop of these few-microsecond launches measures the host's launch rate
+    instead, reported as "us_eager"."""
     import torch
     import sv2hip
 
@@ -231,11 +236,11 @@ def sampler_bench(dev, reps: int = 50):
     dit_in = torch.empty((33,) + shape[1:], device=dev)
     guided = torch.empty_like(lat)
     nxt = torch.empty_like(lat)
-    stream = torch.cuda.current_stream()
+    cur = torch.cuda.current_stream  # the capture stream inside a graph capture
     ops = {
-        "dit_input": (lambda: s.make_dit_input(lat, cond, output=dit_in, stream=stream), 65 * 4 * n // 16),
-        "cfg_rescale": (lambda: s.apply_cfg(pos, neg, 6.5, 0.7, output=guided, stream=stream), 20 * n),
-        "euler_step": (lambda: s.step_to(guided, lat, 980.0, 960.0, output=nxt, stream=stream), 12 * n),
+        "dit_input": (lambda: s.make_dit_input(lat, cond, output=dit_in, stream=cur()), 65 * 4 * n // 16),
+        "cfg_rescale": (lambda: s.apply_cfg(pos, neg, 6.5, 0.7, output=guided, stream=cur()), 20 * n),
+        "euler_step": (lambda: s.step_to(guided, lat, 980.0, 960.0, output=nxt, stream=cur()), 12 * n),
     }
     out = {}
     for name, (fn, nbytes) in ops.items():
@@ -243,13 +248,26 @@ def sampler_bench(dev, reps: int = 50):
             fn()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        a.record(stream)
+        a.record(cur())
         for _ in range(reps):
             fn()
-        b.record(stream)
+        b.record(cur())
+        torch.cuda.synchronize()
+        us_eager = a.elapsed_time(b) * 1e3 / reps
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a.record(cur())
+        graph.replay()
+        b.record(cur())
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / reps
-        out[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+        del graph
+        out[name] = {"us": round(us, 2), "us_eager": round(us_eager, 2), "bytes": nbytes,
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "hbm_util": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
     out["step_us"] = round(sum(v["us"] for v in out.values()), 2)
     out["workload"] = "sampler step at 1280x720x21: latent 16x6x90x160 fp32, CFG 6.5 rescale 0.7, Euler 980->960"
