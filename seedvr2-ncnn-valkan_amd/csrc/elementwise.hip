@@ -16,6 +16,8 @@ using namespace vec;
 
 // Most 8-element vectors one lane keeps in registers per row (dim <= 8*64*kMaxVec).
 constexpr int kMaxVec = 8;
+// The same for rows of up to 2560 channels (fewer registers, more waves).
+constexpr int kNarrowVec = 5;
 
 // Operands of the ada modulation for 8 consecutive channels c0..c0+7.
 //   input:  mul[c] = emb[c*6+slot+1] + scale[c], e0[c] = emb[c*6+slot], sh[c] = shift[c]
@@ -80,76 +82,132 @@ struct TableGate
     }
 };
 
-// One wave per row.  Follows apply_rmsnorm + apply_ada_input
-// (seedvr2_dit_block.cpp:770-805): a double sum of squares, inv =
-// 1/sqrtf(float(ss/dim) + eps), x *= inv, then
+// Rows of one workgroup (4 waves, one row at a time per wave).
+constexpr int kNormRowsPerBlock = 16;
+
+// Follows apply_rmsnorm + apply_ada_input (seedvr2_dit_block.cpp:770-805): a
+// double sum of squares, inv = 1/sqrtf(float(ss/dim) + eps), x *= inv, then
 // x = x*(emb[c*6+slot+1] + scale[c]) + emb[c*6+slot] + shift[c] evaluated left
 // to right in fp32 with no fused multiply-add.  With `gamma` (the DiT output
 // head's norm weight, seedvr2_dit_output.cpp:372-384) x = (x * inv) * gamma[c]
-// before the modulation.  The row stays in registers between the reduction
-// and the write, so HBM sees one read and one write.
-template <typename T, typename Mod>
+// before the modulation.  A row stays in registers between the reduction and
+// the write, so HBM sees one read and one write.  The workgroup stages the
+// modulation vectors (and gamma) in LDS once for its 16 rows, so they are
+// read from L2 once per 16 rows rather than once per row.  LDS: `tables`
+// floats [mul | e0 | shift | gamma] of dim each (the ones in use).
+template <typename T, typename Mod, int kVec>
 __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y, int rows, int dim, float eps,
                                                           Mod mod, const float* gamma, int has_ada)
 {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows)
-        return;
-    const int nvec = dim / 8;
-    const long long base = static_cast<long long>(row) * dim;
-    float v[kMaxVec][8];
-    double ss = 0.0;
-#pragma unroll
-    for (int k = 0; k < kMaxVec; k++)
+    extern __shared__ __attribute__((aligned(16))) float tab[];
+    float* t_mul = tab;
+    float* t_e0 = tab + dim;
+    float* t_sh = tab + 2 * dim;
+    float* t_gm = tab + (has_ada ? 3 * dim : 0);
+    for (int c0 = threadIdx.x * 8; c0 < dim; c0 += 256 * 8)
     {
-        const int vi = lane + 64 * k;
-        if (vi < nvec)
+        if (has_ada)
         {
-            ld8<T>(x, base + vi * 8, v[k]);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                ss += static_cast<double>(v[k][e]) * static_cast<double>(v[k][e]);
+            float mul[8], e0[8], sh[8];
+            mod.load(c0, mul, e0, sh);
+            st8<F32>(t_mul, c0, mul);
+            st8<F32>(t_e0, c0, e0);
+            st8<F32>(t_sh, c0, sh);
+        }
+        if (gamma)
+        {
+            float gm[8];
+            ld8<F32>(gamma, c0, gm);
+            st8<F32>(t_gm, c0, gm);
         }
     }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nvec = dim / 8;
+    // each wave's next row is loaded while the current one is reduced and
+    // written, so two rows per wave are in flight
+    Raw8<T> cur[kVec];
+    Raw8<T> nxt[kVec];
+    int row = blockIdx.x * kNormRowsPerBlock + wave;
+    if (row >= rows)
+        return;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1)
-        ss += __shfl_xor(ss, m);
-    const float inv = 1.f / sqrtf(static_cast<float>(ss / dim) + eps);
-#pragma unroll
-    for (int k = 0; k < kMaxVec; k++)
+    for (int k = 0; k < kVec; k++)
+        if (lane + 64 * k < nvec)
+            ld_raw8<T>(x, static_cast<long long>(row) * dim + (lane + 64 * k) * 8, cur[k]);
+    for (int r = 0; r < kNormRowsPerBlock / 4; r++, row += 4)
     {
-        const int vi = lane + 64 * k;
-        if (vi < nvec)
+        const bool more = r + 1 < kNormRowsPerBlock / 4 && row + 4 < rows;
+        if (more)
         {
-            const int c0 = vi * 8;
-            float out[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                out[e] = v[k][e] * inv;
-            if (gamma)
-            {
-                float gm[8];
-                ld8<F32>(gamma, c0, gm);
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    out[e] = out[e] * gm[e];
-            }
-            if (has_ada)
-            {
-                float mul[8], e0[8], sh[8];
-                mod.load(c0, mul, e0, sh);
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                {
-                    const float add1 = out[e] * mul[e];
-                    const float add2 = add1 + e0[e];
-                    out[e] = add2 + sh[e];
-                }
-            }
-            st8<T>(y, base + c0, out);
+            for (int k = 0; k < kVec; k++)
+                if (lane + 64 * k < nvec)
+                    ld_raw8<T>(x, static_cast<long long>(row + 4) * dim + (lane + 64 * k) * 8, nxt[k]);
         }
+        const long long base = static_cast<long long>(row) * dim;
+        float v[kVec][8];
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < kVec; k++)
+        {
+            const int vi = lane + 64 * k;
+            if (vi < nvec)
+            {
+                raw8_float(cur[k], v[k]);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    ss += static_cast<double>(v[k][e]) * static_cast<double>(v[k][e]);
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1)
+            ss += __shfl_xor(ss, m);
+        const float inv = 1.f / sqrtf(static_cast<float>(ss / dim) + eps);
+#pragma unroll
+        for (int k = 0; k < kVec; k++)
+        {
+            const int vi = lane + 64 * k;
+            if (vi < nvec)
+            {
+                const int c0 = vi * 8;
+                float out[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    out[e] = v[k][e] * inv;
+                if (gamma)
+                {
+                    float gm[8];
+                    ld8<F32>(t_gm, c0, gm);
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        out[e] = out[e] * gm[e];
+                }
+                if (has_ada)
+                {
+                    float mul[8], e0[8], sh[8];
+                    ld8<F32>(t_mul, c0, mul);
+                    ld8<F32>(t_e0, c0, e0);
+                    ld8<F32>(t_sh, c0, sh);
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                    {
+                        const float add1 = out[e] * mul[e];
+                        const float add2 = add1 + e0[e];
+                        out[e] = add2 + sh[e];
+                    }
+                }
+                st8<T>(y, base + c0, out);
+            }
+        }
+        if (!more)
+            return;
+#pragma unroll
+        for (int k = 0; k < kVec; k++)
+            cur[k] = nxt[k];
     }
 }
 
@@ -335,16 +393,40 @@ int launch_rmsnorm(const void* x, void* y, int dtype, int rows, int dim, float e
 {
     if (rows == 0)
         return SV2_OK;
-    const dim3 grid((rows + 3) / 4);
+    if (dim <= 0 || dim % 8 != 0 || dim > 8 * 64 * kMaxVec)
+        return set_error(SV2_EUNSUPPORTED, "rmsnorm_ada: dim must be a multiple of 8 and <= 4096");
+    const dim3 grid((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+    const size_t lds = static_cast<size_t>((has_ada ? 3 : 0) + (gamma ? 1 : 0)) * dim * sizeof(float);
+    // rows of up to 2560 channels (the 3B model's width) keep 5 vectors per
+    // lane in registers, wider ones up to kMaxVec
+    const bool narrow = dim <= 8 * 64 * kNarrowVec;
     if (dtype == SV2_F32)
-        hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
-                           gamma, has_ada);
+    {
+        if (narrow)
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+        else
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+    }
     else if (dtype == SV2_F16)
-        hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
-                           gamma, has_ada);
+    {
+        if (narrow)
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+        else
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+    }
     else
-        hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod>), grid, dim3(256), 0, stream, x, y, rows, dim, eps, mod,
-                           gamma, has_ada);
+    {
+        if (narrow)
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+        else
+            hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
+                               dim, eps, mod, gamma, has_ada);
+    }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
 }

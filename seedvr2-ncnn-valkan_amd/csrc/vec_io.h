@@ -87,6 +87,58 @@ __device__ inline void ld8<BF16>(const void* base, long long i, float x[8])
         x[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
     }
 }
+// The raw bytes of 8 elements (16 for fp16 / bf16, 32 for fp32), for kernels
+// that keep data in flight in registers before converting it.
+template <typename T>
+struct Raw8
+{
+    uint4 r[1];
+};
+template <>
+struct Raw8<F32>
+{
+    uint4 r[2];
+};
+
+template <typename T>
+__device__ inline void ld_raw8(const void* base, long long i, Raw8<T>& v)
+{
+    constexpr int n = sizeof(Raw8<T>) / sizeof(uint4);
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(base) + i * 2 * n);
+#pragma unroll
+    for (int k = 0; k < n; k++)
+        v.r[k] = p[k];
+}
+
+__device__ inline void raw8_float(const Raw8<F32>& v, float x[8])
+{
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+    {
+        x[4 * k] = __builtin_bit_cast(float, v.r[k].x);
+        x[4 * k + 1] = __builtin_bit_cast(float, v.r[k].y);
+        x[4 * k + 2] = __builtin_bit_cast(float, v.r[k].z);
+        x[4 * k + 3] = __builtin_bit_cast(float, v.r[k].w);
+    }
+}
+__device__ inline void raw8_float(const Raw8<F16>& v, float x[8])
+{
+    const f16x8 h = __builtin_bit_cast(f16x8, v.r[0]);
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        x[e] = static_cast<float>(h[e]);
+}
+__device__ inline void raw8_float(const Raw8<BF16>& v, float x[8])
+{
+    const uint32_t w[4] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+    {
+        x[2 * e] = __builtin_bit_cast(float, w[e] << 16);
+        x[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
+    }
+}
+
 template <>
 __device__ inline void st8<BF16>(void* base, long long i, const float x[8])
 {
