@@ -12,6 +12,7 @@
 
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <tuple>
 
@@ -82,13 +83,28 @@ struct LtPlan
     hipblasLtMatmulAlgo_t algo{};
 };
 
-using PlanKey = std::tuple<int, int, int, int>; // device, rows, in, out
+using PlanKey = std::tuple<int, int, int, int, int>; // device, rows, in, out, gated
+
+// The gated form: D = gate[c] * (X W^T)[r][c] + R[r][c] (alpha a device vector
+// over the output channels, beta 1, C = the residual R).
+struct Gated
+{
+    const float* gate = nullptr;
+    const void* residual = nullptr;
+};
 
 int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out, const void* x, const void* w,
-              void* y, LtPlan* plan)
+              void* y, const Gated* gated, LtPlan* plan)
 {
     if (hipblasLtMatmulDescCreate(&plan->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
         return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmulDescCreate failed");
+    if (gated)
+    {
+        const int32_t mode = HIPBLASLT_POINTER_MODE_ALPHA_DEVICE_VECTOR_BETA_HOST;
+        if (hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &mode, sizeof(mode)) !=
+            HIPBLAS_STATUS_SUCCESS)
+            return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no per-channel alpha");
+    }
     const hipblasOperation_t ta = HIPBLAS_OP_T;
     const hipblasOperation_t tb = HIPBLAS_OP_N;
     if (hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) !=
@@ -113,8 +129,11 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
     hipblasLtMatmulPreferenceDestroy(pref);
     if (hs != HIPBLAS_STATUS_SUCCESS || got <= 0)
         return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no kernel for an fp16 product of this shape");
-    const float alpha = 1.f;
-    const float beta = 0.f;
+    const float one = 1.f;
+    const float zero = 0.f;
+    const void* alpha = gated ? static_cast<const void*>(gated->gate) : &one;
+    const float* beta = gated ? &one : &zero;
+    const void* c = gated ? gated->residual : y;
     hipEvent_t e0 = nullptr;
     hipEvent_t e1 = nullptr;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
@@ -124,11 +143,11 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
     {
         if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize != 0)
             continue;
-        bool ok = hipblasLtMatmul(h, plan->desc, &alpha, w, plan->a, x, plan->b, &beta, y, plan->d, y, plan->d,
+        bool ok = hipblasLtMatmul(h, plan->desc, alpha, w, plan->a, x, plan->b, beta, c, plan->d, y, plan->d,
                                   &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
         ok = ok && hipEventRecord(e0, stream) == hipSuccess;
         for (int r = 0; r < 3 && ok; r++)
-            ok = hipblasLtMatmul(h, plan->desc, &alpha, w, plan->a, x, plan->b, &beta, y, plan->d, y, plan->d,
+            ok = hipblasLtMatmul(h, plan->desc, alpha, w, plan->a, x, plan->b, beta, c, plan->d, y, plan->d,
                                  &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
         ok = ok && hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
         float ms = 0.f;
@@ -143,11 +162,13 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (best < 0.f)
-        return set_error(SV2_EDEVICE, "gemm: no hipBLASLt kernel ran for an fp16 product of this shape");
+        return set_error(gated ? SV2_EUNSUPPORTED : SV2_EDEVICE,
+                         "gemm: no hipBLASLt kernel ran for an fp16 product of this shape");
     return SV2_OK;
 }
 
-int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y)
+int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y,
+             const Gated* gated = nullptr)
 {
     int rc = SV2_OK;
     LtPlan plan;
@@ -161,20 +182,30 @@ int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const
         if (!h)
             return rc;
         static std::map<PlanKey, LtPlan> plans;
-        const PlanKey key{device, rows, in, out};
+        static std::set<PlanKey> unsupported; // gated shapes the library has no kernel for
+        const PlanKey key{device, rows, in, out, gated ? 1 : 0};
+        if (unsupported.count(key))
+            return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no gated kernel for this shape");
         auto it = plans.find(key);
         if (it == plans.end())
         {
             LtPlan fresh;
-            if ((rc = make_plan(h, stream, rows, in, out, x, w, y, &fresh)) != SV2_OK)
+            if ((rc = make_plan(h, stream, rows, in, out, x, w, y, gated, &fresh)) != SV2_OK)
+            {
+                if (gated && rc == SV2_EUNSUPPORTED)
+                    unsupported.insert(key);
                 return rc;
+            }
             it = plans.emplace(key, fresh).first;
         }
         plan = it->second;
     }
-    const float alpha = 1.f;
-    const float beta = 0.f;
-    if (hipblasLtMatmul(h, plan.desc, &alpha, w, plan.a, x, plan.b, &beta, y, plan.d, y, plan.d, &plan.algo, nullptr,
+    const float one = 1.f;
+    const float zero = 0.f;
+    const void* alpha = gated ? static_cast<const void*>(gated->gate) : &one;
+    const float* beta = gated ? &one : &zero;
+    const void* c = gated ? gated->residual : y;
+    if (hipblasLtMatmul(h, plan.desc, alpha, w, plan.a, x, plan.b, beta, c, plan.d, y, plan.d, &plan.algo, nullptr,
                         0, stream) != HIPBLAS_STATUS_SUCCESS)
         return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmul failed");
     return SV2_OK;
@@ -204,6 +235,17 @@ int gemm_f32(hipStream_t stream, int rows, int in, int out, const void* x, const
 }
 
 } // namespace
+
+int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y,
+                    const float* gate, const void* residual)
+{
+    if (dtype != SV2_F16)
+        return set_error(SV2_EUNSUPPORTED, "gemm: the gated product runs on fp16 only");
+    if (rows == 0)
+        return SV2_OK;
+    const Gated g{gate, residual};
+    return gemm_f16(stream, rows, in, out, x, w, y, &g);
+}
 
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y)
 {

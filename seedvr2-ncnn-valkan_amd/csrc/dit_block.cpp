@@ -323,6 +323,13 @@ int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, cons
         return rc;
     if ((rc = sv2_swiglu(g, u, dt, static_cast<int64_t>(rows) * F, stream)) != SV2_OK)
         return rc;
+    if (dt == SV2_F16)
+    {
+        // the gated residual in the out product's epilogue
+        rc = gemm_rows_gated(stream, dt, rows, F, D, g, br.w_out, out, table + 2 * D, x);
+        if (rc != SV2_EUNSUPPORTED)
+            return rc;
+    }
     if ((rc = gemm_rows(stream, dt, rows, F, D, g, br.w_out, out)) != SV2_OK)
         return rc;
     return launch_residual_table(out, x, dt, rows, D, table, nullptr, 0, stream);
