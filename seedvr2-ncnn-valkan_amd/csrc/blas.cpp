@@ -5,7 +5,9 @@
 // need no workspace, times each on the caller's stream with the caller's
 // buffers and keeps the fastest for the rest of the process; that first call
 // therefore synchronises the stream once.  Without a workspace, products on
-// different streams share nothing.
+// different streams share nothing.  The gated form carries the block's gated
+// residual in the library's epilogue (per-channel alpha, beta 1, optional
+// bias), planned per shape in the same way.
 // fp32 (the parity mode): rocBLAS gemm_ex.
 #include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
@@ -85,12 +87,14 @@ struct LtPlan
 
 using PlanKey = std::tuple<int, int, int, int, int>; // device, rows, in, out, gated
 
-// The gated form: D = gate[c] * (X W^T)[r][c] + R[r][c] (alpha a device vector
-// over the output channels, beta 1, C = the residual R).
+// The gated form: D = gate[c] * (X W^T)[r][c] + R[r][c] (+ bias[c]) (alpha a
+// device vector over the output channels, beta 1, C = the residual R, the
+// library's bias epilogue added after the alpha scaling).
 struct Gated
 {
     const float* gate = nullptr;
     const void* residual = nullptr;
+    const float* bias = nullptr;
 };
 
 int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out, const void* x, const void* w,
@@ -104,6 +108,18 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
         if (hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &mode, sizeof(mode)) !=
             HIPBLAS_STATUS_SUCCESS)
             return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no per-channel alpha");
+        if (gated->bias)
+        {
+            const hipblasLtEpilogue_t epi = HIPBLASLT_EPILOGUE_BIAS;
+            const int32_t bias_type = HIP_R_32F;
+            if (hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)) !=
+                    HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bias_type,
+                                                sizeof(bias_type)) != HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatmulDescSetAttribute(plan->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &gated->bias,
+                                                sizeof(gated->bias)) != HIPBLAS_STATUS_SUCCESS)
+                return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no fp32 bias epilogue");
+        }
     }
     const hipblasOperation_t ta = HIPBLAS_OP_T;
     const hipblasOperation_t tb = HIPBLAS_OP_N;
@@ -183,7 +199,7 @@ int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const
             return rc;
         static std::map<PlanKey, LtPlan> plans;
         static std::set<PlanKey> unsupported; // gated shapes the library has no kernel for
-        const PlanKey key{device, rows, in, out, gated ? 1 : 0};
+        const PlanKey key{device, rows, in, out, gated ? (gated->bias ? 2 : 1) : 0};
         if (unsupported.count(key))
             return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no gated kernel for this shape");
         auto it = plans.find(key);
@@ -199,6 +215,19 @@ int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const
             it = plans.emplace(key, fresh).first;
         }
         plan = it->second;
+        // the bias pointer is a property of the shared descriptor: set it for
+        // this call while the lock is held, and enqueue under the lock
+        if (gated && gated->bias)
+        {
+            if (hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &gated->bias,
+                                                sizeof(gated->bias)) != HIPBLAS_STATUS_SUCCESS)
+                return set_error(SV2_EDEVICE, "gemm: hipBLASLt bias pointer");
+            const float one = 1.f;
+            if (hipblasLtMatmul(h, plan.desc, gated->gate, w, plan.a, x, plan.b, &one, gated->residual, plan.d, y,
+                                plan.d, &plan.algo, nullptr, 0, stream) != HIPBLAS_STATUS_SUCCESS)
+                return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmul failed");
+            return SV2_OK;
+        }
     }
     const float one = 1.f;
     const float zero = 0.f;
@@ -237,13 +266,13 @@ int gemm_f32(hipStream_t stream, int rows, int in, int out, const void* x, const
 } // namespace
 
 int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y,
-                    const float* gate, const void* residual)
+                    const float* gate, const void* residual, const float* bias)
 {
     if (dtype != SV2_F16)
         return set_error(SV2_EUNSUPPORTED, "gemm: the gated product runs on fp16 only");
     if (rows == 0)
         return SV2_OK;
-    const Gated g{gate, residual};
+    const Gated g{gate, residual, bias};
     return gemm_f16(stream, rows, in, out, x, w, y, &g);
 }
 

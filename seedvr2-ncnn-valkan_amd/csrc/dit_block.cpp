@@ -268,8 +268,10 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
     if (attn < 0)
         return static_cast<int>(attn);
     size_t off = 0;
-    w->tables = off; // four ada tables [3][D] fp32: video attention, video MLP, text attention, text MLP
-    off = align256(off + 12 * D * sizeof(float));
+    // four ada tables [3][D] fp32 (video attention, video MLP, text attention,
+    // text MLP), then the video projection's bias times its gate [D]
+    w->tables = off;
+    off = align256(off + 13 * D * sizeof(float));
     w->xa = off;
     off = align256(off + R * D * es);
     w->qkv_v = off;
@@ -666,12 +668,31 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     }
     else
     {
-        if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
-            return rc;
-        if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
-            return rc;
-        if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
-            return rc;
+        // fp16 without debug captures: the gated residual (bias moved past the
+        // gate) in the product's epilogue
+        rc = SV2_EUNSUPPORTED;
+        if (dt == SV2_F16 && !dbg && Lv > 0)
+        {
+            float* gated_bias = nullptr;
+            if (vb.b_proj)
+            {
+                gated_bias = tables + 12 * D;
+                if ((rc = launch_gated_bias(tab_va + 2 * D, vb.b_proj, gated_bias, D, stream)) != SV2_OK)
+                    return rc;
+            }
+            rc = gemm_rows_gated(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v, tab_va + 2 * D, vid, gated_bias);
+            if (rc != SV2_OK && rc != SV2_EUNSUPPORTED)
+                return rc;
+        }
+        if (rc == SV2_EUNSUPPORTED)
+        {
+            if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
+                return rc;
+            if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
+                return rc;
+            if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
+                return rc;
+        }
     }
     if (Lt > 0)
     {

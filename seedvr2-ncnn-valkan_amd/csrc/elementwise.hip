@@ -282,6 +282,16 @@ __global__ __launch_bounds__(256) void ada_table_kernel(const float* emb, const 
         out[2 * dim + c] = emb[c * 6 + slot + 2] + gate[c];
 }
 
+// out[c] = gate[c] * bias[c]: an InnerProduct bias moved past the gate, for a
+// product that adds it after its per-channel scaling.
+__global__ __launch_bounds__(256) void gated_bias_kernel(const float* gate, const float* bias, float* out, int dim)
+{
+#pragma clang fp contract(off)
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < dim)
+        out[c] = gate[c] * bias[c];
+}
+
 // silu(g) * v with silu(g) = g / (1 + exp(-g)) (seedvr2_dit_block.cpp:58-61, :1103-1109).
 template <typename T>
 __global__ __launch_bounds__(256) void swiglu_kernel(void* gate, const void* value, long long count)
@@ -450,6 +460,15 @@ int launch_residual(void* x, const void* residual, int dtype, int rows, int dim,
                            gate, bias, mode);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "ada_residual_kernel launch");
+}
+
+int launch_gated_bias(const float* gate, const float* bias, float* out, int dim, hipStream_t stream)
+{
+    if (dim <= 0)
+        return set_error(SV2_EINVAL, "gated_bias: bad dim");
+    hipLaunchKernelGGL(gated_bias_kernel, dim3((dim + 255) / 256), dim3(256), 0, stream, gate, bias, out, dim);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "gated_bias_kernel launch");
 }
 
 int launch_ada_table(const float* emb, const float* scale, const float* gate, int slot, int dim, float* out,

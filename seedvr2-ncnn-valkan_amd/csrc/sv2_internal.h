@@ -132,11 +132,14 @@ int launch_residual_table(void* x, const void* residual, int dtype, int rows, in
 // times the library's candidate kernels and synchronises the stream once),
 // fp32 on rocBLAS.
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y);
-// fp16 only: y = gate[c] * (x W^T)[r][c] + residual[r][c], the gated residual
-// of seedvr2_dit_block.cpp:807-825 in the product's epilogue (fp32, one
-// rounding to fp16); -2 when hipBLASLt has no kernel for it.
+// fp16 only: y = gate[c] * (x W^T)[r][c] + residual[r][c] (+ bias[c] when
+// bias is not null), the gated residual of seedvr2_dit_block.cpp:807-825 in
+// the product's epilogue (fp32, one rounding to fp16); -2 when hipBLASLt has
+// no kernel for it.  A preceding InnerProduct bias b enters as bias = gate * b.
 int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y,
-                    const float* gate, const void* residual);
+                    const float* gate, const void* residual, const float* bias = nullptr);
+// out[c] = gate[c] * bias[c] (fp32, dim channels).
+int launch_gated_bias(const float* gate, const float* bias, float* out, int dim, hipStream_t stream);
 
 // fp16 y = epilogue(x W^T) on the hand-written MFMA kernel (gemm.hip), x
 // [rows][in], W (and w2) [out][in].  Epilogues: store; the gated residual
