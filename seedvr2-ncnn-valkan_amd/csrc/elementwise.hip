@@ -82,8 +82,10 @@ struct TableGate
     }
 };
 
-// Rows of one workgroup (4 waves, one row at a time per wave).
+// Rows of one workgroup (4 waves, one row at a time per wave): 16 when the
+// launch still fills the chip with them, else 4 (one per wave).
 constexpr int kNormRowsPerBlock = 16;
+constexpr int kNormRowsPerBlockFew = 4;
 
 // Follows apply_rmsnorm + apply_ada_input (seedvr2_dit_block.cpp:770-805): a
 // double sum of squares, inv = 1/sqrtf(float(ss/dim) + eps), x *= inv, then
@@ -92,10 +94,11 @@ constexpr int kNormRowsPerBlock = 16;
 // head's norm weight, seedvr2_dit_output.cpp:372-384) x = (x * inv) * gamma[c]
 // before the modulation.  A row stays in registers between the reduction and
 // the write, so HBM sees one read and one write.  The workgroup stages the
-// modulation vectors (and gamma) in LDS once for its 16 rows, so they are
-// read from L2 once per 16 rows rather than once per row.  LDS: `tables`
+// modulation vectors (and gamma) in LDS once for its `rpb` rows (16 on large
+// launches), so they are read from L2 once per 16 rows rather than once per
+// row.  LDS: `tables`
 // floats [mul | e0 | shift | gamma] of dim each (the ones in use).
-template <typename T, typename Mod, int kVec>
+template <typename T, typename Mod, int kVec, int rpb>
 __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y, int rows, int dim, float eps,
                                                           Mod mod, const float* gamma, int has_ada)
 {
@@ -131,16 +134,16 @@ __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y
     // written, so two rows per wave are in flight
     Raw8<T> cur[kVec];
     Raw8<T> nxt[kVec];
-    int row = blockIdx.x * kNormRowsPerBlock + wave;
+    int row = blockIdx.x * rpb + wave;
     if (row >= rows)
         return;
 #pragma unroll
     for (int k = 0; k < kVec; k++)
         if (lane + 64 * k < nvec)
             ld_raw8<T>(x, static_cast<long long>(row) * dim + (lane + 64 * k) * 8, cur[k]);
-    for (int r = 0; r < kNormRowsPerBlock / 4; r++, row += 4)
+    for (int r = 0; r < rpb / 4; r++, row += 4)
     {
-        const bool more = r + 1 < kNormRowsPerBlock / 4 && row + 4 < rows;
+        const bool more = r + 1 < rpb / 4 && row + 4 < rows;
         if (more)
         {
 #pragma unroll
@@ -397,6 +400,22 @@ int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipSt
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "to_f32_kernel launch");
 }
+template <typename Mod, int kVec, int rpb>
+void launch_rmsnorm_rows(const void* x, void* y, int dtype, int rows, int dim, float eps, Mod mod, const float* gamma,
+                         int has_ada, size_t lds, hipStream_t stream)
+{
+    const dim3 grid((rows + rpb - 1) / rpb);
+    if (dtype == SV2_F32)
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod, kVec, rpb>), grid, dim3(256), lds, stream, x, y, rows, dim,
+                           eps, mod, gamma, has_ada);
+    else if (dtype == SV2_F16)
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod, kVec, rpb>), grid, dim3(256), lds, stream, x, y, rows, dim,
+                           eps, mod, gamma, has_ada);
+    else
+        hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod, kVec, rpb>), grid, dim3(256), lds, stream, x, y, rows, dim,
+                           eps, mod, gamma, has_ada);
+}
+
 template <typename Mod>
 int launch_rmsnorm(const void* x, void* y, int dtype, int rows, int dim, float eps, Mod mod, const float* gamma,
                    int has_ada, hipStream_t stream)
@@ -405,38 +424,24 @@ int launch_rmsnorm(const void* x, void* y, int dtype, int rows, int dim, float e
         return SV2_OK;
     if (dim <= 0 || dim % 8 != 0 || dim > 8 * 64 * kMaxVec)
         return set_error(SV2_EUNSUPPORTED, "rmsnorm_ada: dim must be a multiple of 8 and <= 4096");
-    const dim3 grid((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
     const size_t lds = static_cast<size_t>((has_ada ? 3 : 0) + (gamma ? 1 : 0)) * dim * sizeof(float);
     // rows of up to 2560 channels (the 3B model's width) keep 5 vectors per
-    // lane in registers, wider ones up to kMaxVec
+    // lane in registers, wider ones up to kMaxVec; launches too small to fill
+    // the chip with 16-row workgroups take one row per wave
     const bool narrow = dim <= 8 * 64 * kNarrowVec;
-    if (dtype == SV2_F32)
-    {
-        if (narrow)
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-        else
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<F32, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-    }
-    else if (dtype == SV2_F16)
-    {
-        if (narrow)
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-        else
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<F16, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-    }
+    const bool many = rows >= 256 * kNormRowsPerBlock;
+    if (narrow && many)
+        launch_rmsnorm_rows<Mod, kNarrowVec, kNormRowsPerBlock>(x, y, dtype, rows, dim, eps, mod, gamma, has_ada, lds,
+                                                                stream);
+    else if (narrow)
+        launch_rmsnorm_rows<Mod, kNarrowVec, kNormRowsPerBlockFew>(x, y, dtype, rows, dim, eps, mod, gamma, has_ada,
+                                                                   lds, stream);
+    else if (many)
+        launch_rmsnorm_rows<Mod, kMaxVec, kNormRowsPerBlock>(x, y, dtype, rows, dim, eps, mod, gamma, has_ada, lds,
+                                                             stream);
     else
-    {
-        if (narrow)
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod, kNarrowVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-        else
-            hipLaunchKernelGGL((rmsnorm_ada_kernel<BF16, Mod, kMaxVec>), grid, dim3(256), lds, stream, x, y, rows,
-                               dim, eps, mod, gamma, has_ada);
-    }
+        launch_rmsnorm_rows<Mod, kMaxVec, kNormRowsPerBlockFew>(x, y, dtype, rows, dim, eps, mod, gamma, has_ada, lds,
+                                                                stream);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
 }
