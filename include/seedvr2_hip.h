@@ -134,6 +134,14 @@ typedef struct sv2_attn_args {
     float* debug_pre;        /* optional [sum_w S_w, heads*128] fp32: every query's
                                 output before its bf16 rounding, window-sequence order
                                 (video t->y->x then text), NULL to skip */
+    int exact;               /* 0: the MFMA flash kernel.  1 (fp32 qkv only): the
+                                reference CPU layer's arithmetic step for step
+                                (seedvr2_dit_block.cpp:942-1088: double dot products
+                                and output sums in the reference's order, float
+                                scores, correctly rounded exp and weights, the
+                                denominator summed in key order), the fp32 parity
+                                mode; its workspace also holds q, k, v after the
+                                prologue, 3 x [sum_w S_w, heads*128] fp32 */
 } sv2_attn_args;
 
 /* Host.  Bytes of device workspace sv2_window_attention needs for these args
@@ -436,6 +444,16 @@ void sv2_dit_destroy(sv2_dit* dit);
 #define SV2_EPI_SWIGLU 2
 int sv2_inner_product_f16(const void* x, const void* w, const void* w_value, void* y, int rows, int in, int out,
                           int epilogue, const float* bias, const float* gate, const void* residual, void* stream);
+
+/* ---- fp32 InnerProduct of the parity mode.  Replaces the block's ncnn
+ * InnerProduct layers (load_inner_product, seedvr2_dit_block.cpp:27-55) and
+ * the heads' (seedvr2_dit_input.cpp:354-392, seedvr2_dit_output.cpp:388-390)
+ * in fp32: y [rows, out] = float(sum_i double(x_i) * double(w_i) + double(b)),
+ * the exact products of each output added in increasing i, then the bias
+ * (NULL: none), one rounding to float.  x fp32 [rows, in], W fp32 [out, in]
+ * row-major, bias fp32 [out].  Any shape; y may not alias x or W. */
+int sv2_inner_product_f32(const float* x, const float* w, const float* bias, float* y, int rows, int in, int out,
+                          void* stream);
 
 /* ---- Euler sampler (src/model/sampler.h:18-78) and the latent preparation
  * of the engine loop (src/core/engine.cpp:79-149, :306-350).  Latents are

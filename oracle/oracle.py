@@ -89,6 +89,8 @@ def load() -> ctypes.CDLL:
     vp, i = ctypes.c_void_p, ctypes.c_int
     lib.orc_bf16.argtypes = [ctypes.c_float]
     lib.orc_bf16.restype = ctypes.c_float
+    lib.orc_expf.argtypes = [ctypes.c_float]
+    lib.orc_expf.restype = ctypes.c_float
     lib.orc_bf16_array.argtypes = [vp, vp, ctypes.c_int64]
     lib.orc_adaptive_window.argtypes = [i, i, i, vp, vp, vp]
     lib.orc_make_windows.argtypes = [i, i, i, i, i, i, i, vp, i]
@@ -140,6 +142,11 @@ def _p(a):
 
 def bf16(x: float) -> float:
     return load().orc_bf16(ctypes.c_float(x))
+
+
+def expf(x: float) -> float:
+    """The oracle's std::exp of a float (correctly rounded)."""
+    return load().orc_expf(ctypes.c_float(x))
 
 
 def bf16_array(x):

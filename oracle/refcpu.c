@@ -27,6 +27,14 @@ float orc_bf16(float value)
     return value;
 }
 
+/* The reference's std::exp(float) (seedvr2_dit_block.cpp:58-61, :1059),
+ * correctly rounded: exp in double (error well below 2^-29 of the float
+ * rounding step) rounded once to float. */
+float orc_expf(float x)
+{
+    return (float)exp((double)x);
+}
+
 void orc_bf16_array(const float* in, float* out, int64_t count)
 {
     for (int64_t i = 0; i < count; i++)
@@ -336,7 +344,7 @@ int orc_window_attention(const orc_attn_cfg* cfg, int T, int H, int W, int Lt,
                     float denominator = 0.f;
                     for (int key = 0; key < seq; key++)
                     {
-                        scores[key] = expf(scores[key] - maximum);
+                        scores[key] = orc_expf(scores[key] - maximum);
                         denominator += scores[key];
                     }
                     /* per output dim the sum runs over keys in key order, exactly
@@ -433,7 +441,7 @@ void orc_swiglu(float* gate, const float* value, int64_t count)
     for (int64_t i = 0; i < count; i++)
     {
         const float g = gate[i];
-        gate[i] = (g / (1.f + expf(-g))) * value[i];
+        gate[i] = (g / (1.f + orc_expf(-g))) * value[i];
     }
 }
 
@@ -676,7 +684,7 @@ done:
 
 static float silu_f(float v)
 {
-    return v / (1.f + expf(-v));
+    return v / (1.f + orc_expf(-v));
 }
 
 /* seedvr2_dit_input.cpp:311-403 */

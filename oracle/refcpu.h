@@ -14,6 +14,14 @@
  * window order.  Build with -ffp-contract=off so no multiply-add is fused
  * (the reference is built for baseline x86-64, which has no FMA).
  *
+ * exp: the reference calls std::exp on floats (softmax :1059, silu :58-61),
+ * i.e. the platform libm's expf, whose last bit depends on the libm (glibc
+ * 2.35's expf differs from the correctly rounded value for 6.3e-4 of the
+ * arguments in [-32, 8], by one ulp).  The oracle evaluates the correctly
+ * rounded value, orc_expf(x) = (float)exp((double)x), the libm-independent
+ * result every conforming expf approximates; it is pinned against float64
+ * numpy and against the host libm's expf (at most one ulp apart).
+ *
  * Pinning status (what checks each function beyond its own formula):
  *   orc_bf16            exhaustive-by-class test against torch's bfloat16 cast
  *   orc_make_windows    hand-derived known-answer plans, partition invariants,
@@ -68,6 +76,9 @@ enum {
 
 /* bf16 round-to-nearest-even kept in an fp32 container (seedvr2_dit_block.cpp:68-79). */
 float orc_bf16(float value);
+
+/* std::exp of a float, correctly rounded: (float)exp((double)x). */
+float orc_expf(float x);
 
 /* orc_bf16 over an array (for exhaustive tests of the rounding rule). */
 void orc_bf16_array(const float* in, float* out, int64_t count);

@@ -64,7 +64,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         objs = list(pool.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objs),
-           "-L/opt/rocm/lib", "-lhipblaslt", "-lrocblas", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
+           "-L/opt/rocm/lib", "-lhipblaslt", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

@@ -6,8 +6,8 @@
 //
 //   text_prepare_kernel   the q/k prologue of the L_txt text tokens, once per
 //                         layer (their RoPE positions (l, l, l) do not depend
-//                         on the window): bf16 q/k and transposed fp16 v into
-//                         the workspace;
+//                         on the window): bf16 q/k and transposed v (in the
+//                         P*V operand type) into the workspace;
 //   window_attention_kernel
 //                         one 12-wave workgroup per (window, head) and up to
 //                         384 query rows (windows with more rows split them
@@ -20,13 +20,15 @@
 //                         ahead: waves 0-7 fetch the key tile and run the k
 //                         prologue (RMSNorm * gamma, RoPE, bf16) in place,
 //                         waves 8-11 fetch the value tile and write v, rounded
-//                         to bf16 and held as fp16, transposed.  Each wave
+//                         to bf16, transposed.  Each wave
 //                         owns 32 query rows whose q prologue runs in
 //                         registers.  S^T = K Q^T on bf16 MFMA (exact
 //                         operands), online softmax per 32-key subtile in fp32
 //                         with lazy rescaling (row max / sum exchanged between
 //                         half-waves with v_permlane32_swap), O^T += V^T P^T on
-//                         fp16 MFMA.  Ragged windows: keys past the window are
+//                         fp16 MFMA (fp16 inputs: P and V as fp16) or bf16 MFMA
+//                         (fp32 / bf16 inputs: exact bf16 V, P split into 3 / 2
+//                         bf16 terms).  Ragged windows: keys past the window are
 //                         masked, query rows past it are not stored.  Video
 //                         outputs are written once (the windows partition the
 //                         grid), text outputs to per-window bf16 partials;
@@ -74,20 +76,38 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- element types
 
+// kPTerms: how P enters O^T += V^T P^T.  1: P rounded to fp16 against V held
+// as fp16 (the bf16-rounded values, exact in fp16 within its range) on the
+// fp16 MFMA.  2 or 3: V held as its exact bf16 value and P split into that
+// many bf16 terms (hi + mid [+ lo], each the rounded remainder of the last),
+// one bf16 MFMA per term: 16 or 24 significant bits of P and no fp16 range
+// limit on V.  The fp32 input mode is the parity mode and takes 3 terms.
+//
+// kExact: the q/k prologue follows the reference's arithmetic step for step
+// (double sum of squares, float(sum / 128), correctly rounded fp32 sqrt and
+// divide, unfused products): the fp32 and bf16 input modes.  The fp16 mode
+// keeps an fp32 sum, the hardware reciprocal square root and fused RoPE
+// products (each may move a q/k element by one bf16 ulp, rarely).
 struct F32
 {
     static constexpr int kVec = 2; // uint4 per 8 elements
     static constexpr bool kDma = false;
+    static constexpr int kPTerms = 3;
+    static constexpr bool kExact = true;
 };
 struct F16
 {
     static constexpr int kVec = 1;
     static constexpr bool kDma = true;
+    static constexpr int kPTerms = 1;
+    static constexpr bool kExact = false;
 };
 struct BF16
 {
     static constexpr int kVec = 1;
     static constexpr bool kDma = true;
+    static constexpr int kPTerms = 2;
+    static constexpr bool kExact = true;
 };
 
 template <typename T>
@@ -269,8 +289,10 @@ struct AttnParams
     float* dbg_pre;         // optional [sum S][D]
     uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
-    uint16_t* txt_vt;       // [heads][128][text_pad] fp16, prepared and transposed
+    uint16_t* txt_vt;       // [heads][128][text_pad] P*V operand type, prepared and transposed
     int ordered;            // windows dispatched in the order of `order` (else in plan order)
+    int exact;              // the reference-order fp64 kernel (fp32 inputs)
+    long long seq_rows;     // sum over windows of S_w (window-sequence rows)
     int16_t order[kMaxOrdered]; // window indices by decreasing video length
 };
 
@@ -315,6 +337,41 @@ __device__ inline float partner_sum(float v)
 {
     float a, b;
     with_partner(v, &a, &b);
+    return a + b;
+}
+
+// The double versions: the two 32-bit halves move through the same lane
+// exchanges.
+template <int kCtrl>
+__device__ inline double dpp_f64(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), kCtrl, 0xF, 0xF,
+                                               false);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                          static_cast<uint32_t>(lo));
+}
+
+__device__ inline double row16_sum_f64(double v)
+{
+    v += dpp_f64<0xB1>(v);
+    v += dpp_f64<0x4E>(v);
+    v += dpp_f64<0x141>(v);
+    v += dpp_f64<0x140>(v);
+    return v;
+}
+
+__device__ inline double partner_sum_f64(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    float lo_a, lo_b, hi_a, hi_b;
+    with_partner(__builtin_bit_cast(float, static_cast<uint32_t>(u)), &lo_a, &lo_b);
+    with_partner(__builtin_bit_cast(float, static_cast<uint32_t>(u >> 32)), &hi_a, &hi_b);
+    const double a = __builtin_bit_cast(double, (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, hi_a)) << 32) |
+                                                    __builtin_bit_cast(uint32_t, lo_a));
+    const double b = __builtin_bit_cast(double, (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, hi_b)) << 32) |
+                                                    __builtin_bit_cast(uint32_t, lo_b));
     return a + b;
 }
 
@@ -365,10 +422,43 @@ __device__ inline float inv_rms(float ss, float eps)
     return __builtin_amdgcn_rsqf(ss * (1.f / 128.f) + eps);
 }
 
+// 1.f / std::sqrt(float(ss / 128) + eps) as the reference evaluates it
+// (seedvr2_dit_block.cpp:947-950) from the double sum of squares ss.  The
+// float sqrt and divide are correctly rounded: each is formed in double and
+// rounded once to float, which for float operands gives the correctly
+// rounded float result (53 >= 2 * 24 + 2 bits).
+__device__ inline float inv_rms_exact(double ss, float eps)
+{
+    const float mean = static_cast<float>(ss * (1.0 / 128.0));
+    const float root = static_cast<float>(__builtin_sqrt(static_cast<double>(mean + eps)));
+    return static_cast<float>(1.0 / static_cast<double>(root));
+}
+
+// Partial double sum of squares of n values (the products are exact in
+// double, so a fused multiply-add rounds as the reference's multiply then add).
+template <int N>
+__device__ inline double square_sum_f64(const float* x)
+{
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < N; e++)
+        ss = __builtin_fma(static_cast<double>(x[e]), static_cast<double>(x[e]), ss);
+    return ss;
+}
+
+// (a, b) -> (a c - b s, b c + a s), each product rounded before the add as in
+// the reference's float expression.
+__device__ inline float2 rotate_unfused(float first, float second, float2 c)
+{
+#pragma clang fp contract(off)
+    return make_float2(first * c.x - second * c.y, second * c.x + first * c.y);
+}
+
 // y = x * inv * gamma, then the rotation of the 4 adjacent pairs of the 8
 // dims (seedvr2_dit_block.cpp:950-971): (a, b) -> (a c - b s, b c + a s).
-// cs(q) gives the (cos, sin) of pair q.
-template <bool kRotate, typename CosSin>
+// cs(q) gives the (cos, sin) of pair q.  kExact: unfused products (the
+// reference's rounding); else one product fused into the add.
+template <bool kRotate, bool kExact, typename CosSin>
 __device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, CosSin cs)
 {
     if (norm)
@@ -385,8 +475,17 @@ __device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv,
             const float2 c = cs(q);
             const float first = x[2 * q];
             const float second = x[2 * q + 1];
-            x[2 * q] = __builtin_fmaf(first, c.x, -(second * c.y));
-            x[2 * q + 1] = __builtin_fmaf(second, c.x, first * c.y);
+            if constexpr (kExact)
+            {
+                const float2 r = rotate_unfused(first, second, c);
+                x[2 * q] = r.x;
+                x[2 * q + 1] = r.y;
+            }
+            else
+            {
+                x[2 * q] = __builtin_fmaf(first, c.x, -(second * c.y));
+                x[2 * q + 1] = __builtin_fmaf(second, c.x, first * c.y);
+            }
         }
     }
 }
@@ -434,6 +533,27 @@ __device__ inline f16x2 bf16_pair_as_f16(float a, float b)
     const uint32_t u = bf16_pair_bits(a, b);
     return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, u << 16),
                                                                 __builtin_bit_cast(float, u & 0xffff0000u)));
+}
+
+// Two values of v rounded to bf16, packed in the operand type of the P*V MFMA
+// of input type TI: fp16 of the bf16 values (one P term) or the bf16 bits.
+template <typename TI>
+__device__ inline uint32_t v_pair_operand(float a, float b)
+{
+    if constexpr (TI::kPTerms == 1)
+        return __builtin_bit_cast(uint32_t, bf16_pair_as_f16(a, b));
+    else
+        return bf16_pair_bits(a, b);
+}
+
+// A P*V operand element back in fp32 (for the prologue debug captures).
+template <typename TI>
+__device__ inline float v_operand_value(uint16_t bits)
+{
+    if constexpr (TI::kPTerms == 1)
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    else
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
 }
 
 // A copy of v the compiler cannot see through.  Lane-derived offsets computed
@@ -607,11 +727,18 @@ __device__ inline void query_finish(const AttnParams& p, const Staged& s, const 
     float inv = 1.f;
     if (p.qk_norm)
     {
-        float ss = 0.f;
+        if constexpr (TI::kExact)
+        {
+            inv = inv_rms_exact(partner_sum_f64(square_sum_f64<64>(x)), p.eps);
+        }
+        else
+        {
+            float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < 64; i++)
-            ss = __builtin_fmaf(x[i], x[i], ss);
-        inv = inv_rms(partner_sum(ss), p.eps);
+            for (int i = 0; i < 64; i++)
+                ss = __builtin_fmaf(x[i], x[i], ss);
+            inv = inv_rms(partner_sum(ss), p.eps);
+        }
     }
     if (!is_video)
         return;
@@ -628,7 +755,7 @@ __device__ inline void query_finish(const AttnParams& p, const Staged& s, const 
     for (int c = 0; c < 8; c++)
     {
         const int d0 = 16 * c + 8 * g;
-        scale_rotate8<RM != SV2_ROPE_NONE>(&x[8 * c], &s.gamma[d0], inv, p.qk_norm != 0, [&](int q) {
+        scale_rotate8<RM != SV2_ROPE_NONE, TI::kExact>(&x[8 * c], &s.gamma[d0], inv, p.qk_norm != 0, [&](int q) {
             int axis_a, slot_a, axis_b, slot_b;
             rope_axis_slot<RM>(16 * c + 2 * q, &axis_a, &slot_a);
             rope_axis_slot<RM>(16 * c + 2 * q + 8, &axis_b, &slot_b);
@@ -681,20 +808,27 @@ __device__ inline KeyRope key_rope(const RopeBase& rb, int d0)
 // Prologue of one key chunk (8 dims of a row whose 128 dims are spread over
 // 16 consecutive lanes, all active): per-head RMSNorm (fp32 sum of squares),
 // gamma, RoPE, bf16 rounding.
-template <int RM>
+template <int RM, bool kExact>
 __device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const KeyRope& kr, float x[8], int d0,
                                   uint32_t packed)
 {
     float inv = 1.f;
     if (p.qk_norm)
     {
-        float ss = 0.f;
+        if constexpr (kExact)
+        {
+            inv = inv_rms_exact(row16_sum_f64(square_sum_f64<8>(x)), p.eps);
+        }
+        else
+        {
+            float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            ss = __builtin_fmaf(x[e], x[e], ss);
-        inv = inv_rms(row16_sum(ss), p.eps);
+            for (int e = 0; e < 8; e++)
+                ss = __builtin_fmaf(x[e], x[e], ss);
+            inv = inv_rms(row16_sum(ss), p.eps);
+        }
     }
-    scale_rotate8<RM != SV2_ROPE_NONE>(x, &s.gamma[kHeadDim + d0], inv, p.qk_norm != 0, [&](int q) {
+    scale_rotate8<RM != SV2_ROPE_NONE, kExact>(x, &s.gamma[kHeadDim + d0], inv, p.qk_norm != 0, [&](int q) {
         const int local = static_cast<int>((packed >> kr.shift[q]) & 1023u);
         return s.rope[kr.off[q] + local * kRopePairSlots];
     });
@@ -705,7 +839,7 @@ __device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const Ke
 
 // Text tokens: q/k prologue with the text branch's gammas and positions
 // (l, l, l) in the reference RoPE mode (text is not rotated in the absolute
-// mode), v rounded to bf16 and stored as fp16, transposed; zero padding up to
+// mode), v rounded to bf16 and stored in the P*V operand type, transposed; zero padding up to
 // text_pad so masked keys multiply finite values.
 template <typename TI, int RM>
 __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
@@ -743,20 +877,28 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
     float ik = 1.f;
     if (p.qk_norm)
     {
-        float sq = 0.f;
-        float sk = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
+        if constexpr (TI::kExact)
         {
-            sq = __builtin_fmaf(q[e], q[e], sq);
-            sk = __builtin_fmaf(k[e], k[e], sk);
+            iq = inv_rms_exact(row16_sum_f64(square_sum_f64<8>(q)), p.eps);
+            ik = inv_rms_exact(row16_sum_f64(square_sum_f64<8>(k)), p.eps);
         }
-        iq = inv_rms(row16_sum(sq), p.eps);
-        ik = inv_rms(row16_sum(sk), p.eps);
+        else
+        {
+            float sq = 0.f;
+            float sk = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+            {
+                sq = __builtin_fmaf(q[e], q[e], sq);
+                sk = __builtin_fmaf(k[e], k[e], sk);
+            }
+            iq = inv_rms(row16_sum(sq), p.eps);
+            ik = inv_rms(row16_sum(sk), p.eps);
+        }
     }
     constexpr bool rotate = RM == SV2_ROPE_REFERENCE;
-    scale_rotate8<rotate>(q, gq, iq, p.qk_norm != 0, cs);
-    scale_rotate8<rotate>(k, gk, ik, p.qk_norm != 0, cs);
+    scale_rotate8<rotate, TI::kExact>(q, gq, iq, p.qk_norm != 0, cs);
+    scale_rotate8<rotate, TI::kExact>(k, gk, ik, p.qk_norm != 0, cs);
     const uint4 qb = to_bf16x8(q);
     const uint4 kb = to_bf16x8(k);
     if (l >= p.text_pad)
@@ -767,14 +909,15 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
         *reinterpret_cast<uint4*>(p.txt_q + o) = qb;
         *reinterpret_cast<uint4*>(p.txt_k + o) = kb;
     }
-    _Float16* vt = reinterpret_cast<_Float16*>(p.txt_vt);
+    // +0.0 is the all-zero pattern in fp16 and bf16 alike
+    uint16_t* vt = p.txt_vt;
 #pragma unroll
     for (int e = 0; e < 8; e += 2)
     {
-        const f16x2 h = bf16_pair_as_f16(v[e], v[e + 1]);
+        const uint32_t h = valid ? v_pair_operand<TI>(v[e], v[e + 1]) : 0u;
         const long long base = (static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l;
-        vt[base] = valid ? h[0] : static_cast<_Float16>(0.f);
-        vt[base + p.text_pad] = valid ? h[1] : static_cast<_Float16>(0.f);
+        vt[base] = static_cast<uint16_t>(h & 0xffffu);
+        vt[base + p.text_pad] = static_cast<uint16_t>(h >> 16);
     }
 }
 
@@ -877,14 +1020,16 @@ __device__ inline void wait_tile_fetch(int wave, bool newer_in_flight)
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt4);
 }
 
-// Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0).
+// Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0) in the
+// P*V operand type of input type TI.
+template <typename TI>
 __device__ inline void store_vt_pair(char* vt, int r, int d0, const float v0[8], const float v1[8])
 {
     uint16_t* t = reinterpret_cast<uint16_t*>(vt);
     const int key = 2 * r;
 #pragma unroll
     for (int e = 0; e < 8; e++)
-        *reinterpret_cast<f16x2*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = bf16_pair_as_f16(v0[e], v1[e]);
+        *reinterpret_cast<uint32_t*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = v_pair_operand<TI>(v0[e], v1[e]);
 }
 
 // 16-bit inputs: the prologue of tile kb, run by the waves that fetched it
@@ -915,7 +1060,7 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
             float x[8];
             raw8_to_float<TI>(raw, x);
             const uint32_t packed = static_cast<uint32_t>(s.rows[min(base + r, last)].y);
-            *slot = key_chunk<RM>(p, s, kr, x, d0, packed);
+            *slot = key_chunk<RM, TI::kExact>(p, s, kr, x, d0, packed);
         }
         return;
     }
@@ -942,7 +1087,7 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
         float v1[8];
         raw8_to_float<TI>(a, v0);
         raw8_to_float<TI>(b, v1);
-        store_vt_pair(vt, r, d0, v0, v1);
+        store_vt_pair<TI>(vt, r, d0, v0, v1);
     }
 }
 
@@ -992,13 +1137,13 @@ __device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry
         float x[8];
         load8<F32>(p.vid_qkv, static_cast<long long>(a.x) * p.row_stride + k_col, x);
         *reinterpret_cast<uint4*>(kt + k_slot_offset(rr, chunk)) =
-            key_chunk<RM>(p, s, kr, x, d0, static_cast<uint32_t>(a.y));
+            key_chunk<RM, F32::kExact>(p, s, kr, x, d0, static_cast<uint32_t>(a.y));
     }
     float v0[8];
     float v1[8];
     load8<F32>(p.vid_qkv, static_cast<long long>(s.rows[min(base + 2 * r, last)].x) * p.row_stride + v_col, v0);
     load8<F32>(p.vid_qkv, static_cast<long long>(s.rows[min(base + 2 * r + 1, last)].x) * p.row_stride + v_col, v1);
-    store_vt_pair(vt, r, d0, v0, v1);
+    store_vt_pair<F32>(vt, r, d0, v0, v1);
 }
 
 // ---------------------------------------------------------------- attention step
@@ -1033,8 +1178,9 @@ __device__ inline ReadBases read_bases(int lane)
     return b;
 }
 
-// One 32-key subtile of the online softmax for the wave's 32 query rows.
-template <int KT>
+// One 32-key subtile of the online softmax for the wave's 32 query rows.  NT
+// is the input type's kPTerms (how P enters the P*V product).
+template <int KT, int NT>
 __device__ inline void attend_subtile(const AttnParams& p, const char* kt, const char* vt, const ReadBases& rb,
                                       const bf16x8 qf[8], int nvalid, int g, f32x16 o[4], float& m_run,
                                       float& l_run)
@@ -1089,6 +1235,50 @@ __device__ inline void attend_subtile(const AttnParams& p, const char* kt, const
         }
     }
     const float bias = m_run * p.score_log2;
+    if constexpr (NT > 1)
+    {
+        // ---- P as NT bf16 terms against exact bf16 V.  Each term is the
+        // bf16 rounding of what the terms before it left over (the remainders
+        // are exact in fp32: a value and its rounding are within a factor of
+        // two), so the terms sum to p within 2^-18 (NT = 2) or 2^-27 (NT = 3)
+        // of p.  The row sum adds the same terms.
+#pragma unroll
+        for (int c2 = 0; c2 < 2; c2++)
+        {
+            bf16x8 va[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                va[dt] = *reinterpret_cast<const bf16x8*>(vt + rb.v[c2 + 2 * (KT ^ (dt & 1))] + dt * 4096);
+            uint32_t bw[NT][4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+            {
+                float r0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c2 + e], p.score_log2, -bias));
+                float r1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c2 + e + 1], p.score_log2, -bias));
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                {
+                    const uint32_t u = bf16_pair_bits(r0, r1);
+                    const float h0 = __builtin_bit_cast(float, u << 16);
+                    const float h1 = __builtin_bit_cast(float, u & 0xffff0000u);
+                    bw[t][e >> 1] = u;
+                    l_run += h0;
+                    l_run += h1;
+                    r0 -= h0;
+                    r1 -= h1;
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+            {
+                const bf16x8 b = __builtin_bit_cast(bf16x8, make_uint4(bw[t][0], bw[t][1], bw[t][2], bw[t][3]));
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[dt], b, o[dt], 0, 0, 0);
+            }
+        }
+        return;
+    }
     // ---- P (fp16), row sums from the same fp16 values, O^T += V^T P^T
 #pragma unroll
     for (int c2 = 0; c2 < 2; c2++)
@@ -1366,9 +1556,9 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
             const char* kt = k_tile(smem, p, kb);
             const char* vt = vt_tile(smem, p, kb);
             const int nv = valid_keys(kb);
-            attend_subtile<0>(p, kt, vt, rdb, qf, nv, g, o, m_run, l_run);
+            attend_subtile<0, TI::kPTerms>(p, kt, vt, rdb, qf, nv, g, o, m_run, l_run);
             if (nv > 32)
-                attend_subtile<1>(p, kt, vt, rdb, qf, nv - 32, g, o, m_run, l_run);
+                attend_subtile<1, TI::kPTerms>(p, kt, vt, rdb, qf, nv - 32, g, o, m_run, l_run);
         }
         if (kb + 1 < gm.nkb)
         {
@@ -1447,7 +1637,7 @@ __global__ __launch_bounds__(256) void text_window_reduce_kernel(const uint32_t*
 
 // Debug / test: q, k, v after the prologue, fp32, window-sequence order, from
 // the device functions the attention kernel runs: queries through the MFMA
-// operand-layout path, keys 16 lanes per row, values as the fp16 operands;
+// operand-layout path, keys 16 lanes per row, values as the P*V operands;
 // text rows from the prepared workspace.  One workgroup (4 waves) per
 // (window, head, 32 rows).
 template <typename TI, int RM>
@@ -1504,17 +1694,17 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
             float v[8];
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + p.dim + d0, k);
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 2LL * p.dim + d0, v);
-            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk<RM>(p, s, kr, k, d0, static_cast<uint32_t>(vr.y)));
+            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk<RM, TI::kExact>(p, s, kr, k, d0, static_cast<uint32_t>(vr.y)));
             if (valid)
             {
 #pragma unroll
                 for (int e = 0; e < 8; e += 2)
                 {
-                    const f16x2 h = bf16_pair_as_f16(v[e], v[e + 1]);
+                    const uint32_t h = v_pair_operand<TI>(v[e], v[e + 1]);
                     k_out[o + e] = static_cast<float>(kb[e]);
                     k_out[o + e + 1] = static_cast<float>(kb[e + 1]);
-                    v_out[o + e] = static_cast<float>(h[0]);
-                    v_out[o + e + 1] = static_cast<float>(h[1]);
+                    v_out[o + e] = v_operand_value<TI>(static_cast<uint16_t>(h & 0xffffu));
+                    v_out[o + e + 1] = v_operand_value<TI>(static_cast<uint16_t>(h >> 16));
                 }
             }
         }
@@ -1522,14 +1712,151 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         {
             const int l = jc - box.vlen;
             const uint16_t* ks = p.txt_k + (static_cast<long long>(head) * p.text_len + l) * kHeadDim + d0;
-            const _Float16* vs = reinterpret_cast<const _Float16*>(p.txt_vt);
+            const uint16_t* vs = p.txt_vt;
 #pragma unroll
             for (int e = 0; e < 8; e++)
             {
                 k_out[o + e] = __builtin_bit_cast(float, static_cast<uint32_t>(ks[e]) << 16);
-                v_out[o + e] = static_cast<float>(vs[(static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l]);
+                v_out[o + e] =
+                    v_operand_value<TI>(vs[(static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l]);
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------- exact mode
+
+constexpr int kExactWaves = 4; // query rows per exact_attention_kernel workgroup, one per wave
+
+// The reference CPU layer's attention core step for step
+// (seedvr2_dit_block.cpp:1045-1079), for the fp32 parity mode.  Inputs are
+// q, k, v after the prologue in window-sequence order ([sum_w S_w][D] fp32
+// holding bf16 values, written by qk_prologue_kernel).  One wave per query
+// row; per query, in the reference's order and rounding:
+//   scores    s_j = float(sum_d double(q_d) * k_jd) * scale, the double sum in
+//             increasing d (lanes split the keys; each lane sums its own);
+//   maximum   m = max_j s_j;
+//   exp       e_j = exp(s_j - m), correctly rounded (formed in double and
+//             rounded once to float);
+//   sum       den = sum_j e_j in float, in increasing j (sequence order:
+//             video keys, then text keys) by one lane;
+//   weights   w_j = e_j / den, correctly rounded (formed in double);
+//   outputs   out_d = bf16(float(sum_j double(w_j) * v_jd)), the double sum in
+//             increasing j (lanes split the dims).
+// The products of two floats are exact in double, so the double sums round
+// exactly as the reference's.  Video outputs go to their grid rows, text
+// outputs to the window's bf16 partials.  LDS: q [4][128], scores [4][sstride]
+// (sstride: the longest window sequence rounded up to a multiple of 4, so
+// every wave's scores start 16-byte aligned).
+__global__ __launch_bounds__(256) void exact_attention_kernel(AttnParams p, const float* __restrict__ q,
+                                                              const float* __restrict__ k,
+                                                              const float* __restrict__ v, int nqg, int sstride,
+                                                              float scale)
+{
+    extern __shared__ __attribute__((aligned(16))) float xsm[];
+    const int blk = blockIdx.x;
+    const int qg = blk % nqg;
+    const int rest = blk / nqg;
+    const int head = rest % p.heads;
+    const int wi = rest / p.heads;
+    const WindowBox box = window_box(p.plan, wi);
+    const int seq = box.vlen + p.text_len;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int query = qg * kExactWaves + wave;
+    if (query >= seq)
+        return; // wave-uniform; the kernel has no workgroup barrier
+    float* qs = xsm + wave * kHeadDim;
+    float* sc = xsm + kExactWaves * kHeadDim + wave * sstride;
+    const long long seq_base = static_cast<long long>(box.vprefix) + static_cast<long long>(wi) * p.text_len;
+    const long long hc = static_cast<long long>(head) * kHeadDim;
+    const float* qrow = q + (seq_base + query) * p.dim + hc;
+    qs[lane] = qrow[lane];
+    qs[lane + 64] = qrow[lane + 64];
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): the row is read back by every lane of this wave
+    __builtin_amdgcn_wave_barrier();
+
+    float mloc = -INFINITY;
+    for (int j = lane; j < seq; j += 64)
+    {
+        const float* krow = k + (seq_base + j) * p.dim + hc;
+        double dot = 0.0;
+        for (int d = 0; d < kHeadDim; d += 4)
+        {
+            const float4 qa = *reinterpret_cast<const float4*>(qs + d);
+            const float4 ka = *reinterpret_cast<const float4*>(krow + d);
+            dot = __builtin_fma(static_cast<double>(qa.x), static_cast<double>(ka.x), dot);
+            dot = __builtin_fma(static_cast<double>(qa.y), static_cast<double>(ka.y), dot);
+            dot = __builtin_fma(static_cast<double>(qa.z), static_cast<double>(ka.z), dot);
+            dot = __builtin_fma(static_cast<double>(qa.w), static_cast<double>(ka.w), dot);
+        }
+        const float sj = static_cast<float>(dot) * scale;
+        sc[j] = sj;
+        mloc = fmaxf(mloc, sj);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        mloc = fmaxf(mloc, __shfl_xor(mloc, o));
+    for (int j = lane; j < seq; j += 64)
+        sc[j] = static_cast<float>(exp(static_cast<double>(sc[j] - mloc)));
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    float den = 0.f;
+    if (lane == 0)
+    {
+        int j = 0;
+        for (; j + 4 <= seq; j += 4)
+        {
+            const float4 e4 = *reinterpret_cast<const float4*>(sc + j);
+            den += e4.x;
+            den += e4.y;
+            den += e4.z;
+            den += e4.w;
+        }
+        for (; j < seq; j++)
+            den += sc[j];
+    }
+    den = __shfl(den, 0);
+    __builtin_amdgcn_wave_barrier();
+    const double dden = static_cast<double>(den);
+    for (int j = lane; j < seq; j += 64)
+        sc[j] = static_cast<float>(static_cast<double>(sc[j]) / dden);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+
+    const bool text = query >= box.vlen;
+    long long out_off;
+    if (!text)
+    {
+        int lt, ly, lx;
+        out_off = static_cast<long long>(window_video_row(p.plan, box, query, &lt, &ly, &lx)) * p.dim + hc;
+    }
+    else
+    {
+        out_off = (static_cast<long long>(wi) * p.text_len + (query - box.vlen)) * p.dim + hc;
+    }
+    const float* vcol = v + seq_base * p.dim + hc;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+    {
+        const int d = lane + 64 * h;
+        double sum = 0.0;
+        for (int j = 0; j < seq; j++)
+            sum = __builtin_fma(static_cast<double>(sc[j]), static_cast<double>(vcol[static_cast<long long>(j) * p.dim + d]),
+                                sum);
+        const float pre = static_cast<float>(sum);
+        const float rounded = bf16_round(pre);
+        if (p.dbg_pre)
+            p.dbg_pre[(seq_base + query) * p.dim + hc + d] = pre;
+        const uint32_t bits = __builtin_bit_cast(uint32_t, rounded);
+        if (text)
+            p.partial[out_off + d] = static_cast<uint16_t>(bits >> 16);
+        else if (p.out_dtype == SV2_F32)
+            static_cast<float*>(p.vid_out)[out_off + d] = rounded;
+        else if (p.out_dtype == SV2_F16)
+            static_cast<_Float16*>(p.vid_out)[out_off + d] = static_cast<_Float16>(rounded);
+        else
+            static_cast<uint16_t*>(p.vid_out)[out_off + d] = static_cast<uint16_t>(bits >> 16);
     }
 }
 
@@ -1556,6 +1883,9 @@ struct Workspace
     int64_t txt_q;
     int64_t txt_k;
     int64_t txt_vt;
+    int64_t seq_q; // exact mode: q, k, v after the prologue, window-sequence order, fp32
+    int64_t seq_k;
+    int64_t seq_v;
     int64_t total;
 };
 
@@ -1576,7 +1906,18 @@ Workspace workspace_layout(const AttnParams& p)
     off = align256(off + static_cast<int64_t>(p.heads) * p.text_len * kHeadDim * 2);
     w.txt_vt = off;
     off = align256(off + static_cast<int64_t>(p.heads) * kHeadDim * p.text_pad * 2);
-    w.total = p.text_len > 0 ? off : 0;
+    if (p.text_len == 0)
+        off = 0;
+    w.seq_q = w.seq_k = w.seq_v = off;
+    if (p.exact)
+    {
+        const int64_t bytes = align256(p.seq_rows * p.dim * 4);
+        w.seq_q = off;
+        w.seq_k = off + bytes;
+        w.seq_v = off + 2 * bytes;
+        off += 3 * bytes;
+    }
+    w.total = off;
     return w;
 }
 
@@ -1640,6 +1981,8 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
         return set_error(SV2_EINVAL, "attention: null qkv pointer");
     if (a->qk_norm && (!a->gamma_q_vid || !a->gamma_k_vid))
         return set_error(SV2_EINVAL, "attention: qk_norm needs the video gamma vectors");
+    if (a->exact && a->qkv_dtype != SV2_F32)
+        return set_error(SV2_EINVAL, "attention: the exact mode takes fp32 qkv");
     std::memset(p, 0, sizeof(*p));
     int rc = build_plan(a->rule, &p->plan);
     if (rc != SV2_OK)
@@ -1712,6 +2055,9 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
     p->rope_tab = reinterpret_cast<const float2*>(a->rope_table);
     p->vid_out = a->vid_out;
     p->dbg_pre = a->debug_pre;
+    p->exact = a->exact ? 1 : 0;
+    p->seq_rows = static_cast<long long>(a->rule.frames) * a->rule.height * a->rule.width +
+                  static_cast<long long>(p->plan.nwin) * a->text_len;
     *smax_out = smax;
     *vmax_out = vmax;
     *rope_rows_out = rope_rows;
@@ -1741,16 +2087,16 @@ void launch_text_prepare(const AttnParams& p, hipStream_t stream)
 template <typename TI, int RM>
 int launch_attention(const AttnParams& p, hipStream_t stream)
 {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&window_attention_kernel<TI, RM>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, p.lds.total);
-    if (err != hipSuccess)
-        return hip_error(err, "window attention: dynamic LDS attribute");
+    const int rc = set_dynamic_lds(reinterpret_cast<const void*>(&window_attention_kernel<TI, RM>), p.lds.total,
+                                   "window attention: dynamic LDS attribute");
+    if (rc != SV2_OK)
+        return rc;
     if (p.text_len > 0)
         launch_text_prepare<TI, RM>(p, stream);
     const int groups = (p.npairs + 7) / 8;
     const unsigned grid = static_cast<unsigned>(groups) * 8u * static_cast<unsigned>(p.nqb);
     hipLaunchKernelGGL((window_attention_kernel<TI, RM>), dim3(grid), dim3(kThreads), p.lds.total, stream, p);
-    err = hipGetLastError();
+    const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "window attention launch");
 }
 
@@ -1797,6 +2143,37 @@ int launch_prologue_rope(const AttnParams& p, int rope_mode, int nrb, float* q_o
     return launch_prologue<TI, SV2_ROPE_NONE>(p, nrb, q_out, k_out, v_out, stream);
 }
 
+// Exact mode: the prologue into the workspace's window-sequence buffers, then
+// exact_attention_kernel (the text reduction follows as in the flash path).
+int launch_exact(const AttnParams& p, const Workspace& w, char* base, int rope_mode, int smax, int vmax,
+                 int rope_rows, hipStream_t stream)
+{
+    AttnParams ps = p;
+    ps.lds = lds_layout_staging(vmax, rope_rows);
+    float* q = reinterpret_cast<float*>(base + w.seq_q);
+    float* k = reinterpret_cast<float*>(base + w.seq_k);
+    float* v = reinterpret_cast<float*>(base + w.seq_v);
+    int rc = launch_prologue_rope<F32>(ps, rope_mode, (smax + 31) / 32, q, k, v, stream);
+    if (rc != SV2_OK)
+        return rc;
+    const int sstride = (smax + 3) & ~3;
+    const int lds = (kExactWaves * kHeadDim + kExactWaves * sstride) * static_cast<int>(sizeof(float));
+    if (lds > kMaxLds)
+        return set_error(SV2_EUNSUPPORTED, "attention (exact): window too long for the LDS of a CU");
+    if ((rc = set_dynamic_lds(reinterpret_cast<const void*>(&exact_attention_kernel), lds,
+                              "attention (exact): dynamic LDS attribute")) != SV2_OK)
+        return rc;
+    const int nqg = (smax + kExactWaves - 1) / kExactWaves;
+    const long long grid = static_cast<long long>(p.plan.nwin) * p.heads * nqg;
+    if (grid >= (1LL << 31))
+        return set_error(SV2_EUNSUPPORTED, "attention (exact): grid too large");
+    const float scale = 1.f / std::sqrt(static_cast<float>(kHeadDim)); // seedvr2_dit_block.cpp:896
+    hipLaunchKernelGGL(exact_attention_kernel, dim3(static_cast<unsigned>(grid)), dim3(kExactWaves * 64), lds, stream,
+                       p, q, k, v, nqg, sstride, scale);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "exact_attention_kernel launch");
+}
+
 } // namespace
 } // namespace sv2
 
@@ -1827,7 +2204,10 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
         return rc;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
 
-    if (args->qkv_dtype == SV2_F32)
+    if (p.exact)
+        rc = launch_exact(p, workspace_layout(p), static_cast<char*>(args->workspace), args->rope_mode, smax, vmax,
+                          rope_rows, stream);
+    else if (args->qkv_dtype == SV2_F32)
         rc = launch_rope<F32>(p, args->rope_mode, stream);
     else if (args->qkv_dtype == SV2_F16)
         rc = launch_rope<F16>(p, args->rope_mode, stream);

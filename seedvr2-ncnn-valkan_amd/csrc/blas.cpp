@@ -8,9 +8,9 @@
 // different streams share nothing.  The gated form carries the block's gated
 // residual in the library's epilogue (per-channel alpha, beta 1, optional
 // bias), planned per shape in the same way.
-// fp32 (the parity mode): rocBLAS gemm_ex.
+// fp32 (the parity mode): gemm_f32_exact (gemm_exact.hip), double
+// accumulation in the order of the CPU restatement, the bias added in double.
 #include <hipblaslt/hipblaslt.h>
-#include <rocblas/rocblas.h>
 
 #include <map>
 #include <mutex>
@@ -37,23 +37,6 @@ int current_device(int* rc)
         return -1;
     }
     return device;
-}
-
-// One rocBLAS handle per device (caller holds g_mutex).
-rocblas_handle rocblas_for(int device, int* rc)
-{
-    static std::map<int, rocblas_handle> handles;
-    auto it = handles.find(device);
-    if (it != handles.end())
-        return it->second;
-    rocblas_handle h = nullptr;
-    if (rocblas_create_handle(&h) != rocblas_status_success)
-    {
-        *rc = set_error(SV2_EDEVICE, "gemm: rocblas_create_handle failed");
-        return nullptr;
-    }
-    handles[device] = h;
-    return h;
 }
 
 // One hipBLASLt handle per device (caller holds g_mutex).
@@ -240,29 +223,6 @@ int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const
     return SV2_OK;
 }
 
-int gemm_f32(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y)
-{
-    int rc = SV2_OK;
-    std::lock_guard<std::mutex> lock(g_mutex);
-    const int device = current_device(&rc);
-    if (device < 0)
-        return rc;
-    rocblas_handle h = rocblas_for(device, &rc);
-    if (!h)
-        return rc;
-    const float alpha = 1.f;
-    const float beta = 0.f;
-    rocblas_set_stream(h, stream);
-    // column-major view: Y^T [out x rows] = W [out x in] * X^T [in x rows]
-    const rocblas_status st =
-        rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, out, rows, in, &alpha, w,
-                        rocblas_datatype_f32_r, in, x, rocblas_datatype_f32_r, in, &beta, y, rocblas_datatype_f32_r,
-                        out, y, rocblas_datatype_f32_r, out, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return set_error(SV2_EDEVICE, std::string("gemm: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
-    return SV2_OK;
-}
-
 } // namespace
 
 int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y,
@@ -278,13 +238,21 @@ int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, co
 
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y)
 {
+    return gemm_rows_bias(stream, dtype, rows, in, out, x, w, nullptr, y);
+}
+
+int gemm_rows_bias(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w,
+                   const float* bias, void* y)
+{
     if (rows == 0)
         return SV2_OK;
-    if (dtype == SV2_F16)
-        return gemm_f16(stream, rows, in, out, x, w, y);
     if (dtype == SV2_F32)
-        return gemm_f32(stream, rows, in, out, x, w, y);
-    return set_error(SV2_EINVAL, "gemm: compute dtype must be fp32 or fp16");
+        return gemm_f32_exact(stream, rows, in, out, static_cast<const float*>(x), static_cast<const float*>(w), bias,
+                              static_cast<float*>(y));
+    if (dtype != SV2_F16)
+        return set_error(SV2_EINVAL, "gemm: compute dtype must be fp32 or fp16");
+    const int rc = gemm_f16(stream, rows, in, out, x, w, y);
+    return (rc != SV2_OK || !bias) ? rc : launch_bias_rows(y, bias, SV2_F16, rows, out, stream);
 }
 
 } // namespace sv2

@@ -393,8 +393,8 @@ int sv2_dit_input_forward(sv2_dit_input* in, const float* video, int channel_maj
     float* h2 = reinterpret_cast<float*>(ws + lay.h2);
     // video: patchify (:336-352), vid_in InnerProduct with bias (:354-358)
     if ((rc = launch_patchify(video, patches, dt, frames, h, w, c.video_channels, channel_major, stream)) != SV2_OK ||
-        (rc = gemm_rows(stream, dt, Lp, 4 * c.video_channels, c.dim, patches, in->w_vid, vid_out)) != SV2_OK ||
-        (rc = launch_bias_rows(vid_out, in->b_vid, dt, Lp, c.dim, stream)) != SV2_OK)
+        (rc = gemm_rows_bias(stream, dt, Lp, 4 * c.video_channels, c.dim, patches, in->w_vid, in->b_vid, vid_out)) !=
+            SV2_OK)
         return rc;
     // text: txt_in InnerProduct with bias
     if (text_len > 0)
@@ -407,18 +407,17 @@ int sv2_dit_input_forward(sv2_dit_input* in, const float* video, int channel_maj
                 return rc;
             x = ws + lay.text;
         }
-        if ((rc = gemm_rows(stream, dt, text_len, c.text_channels, c.dim, x, in->w_txt, txt_out)) != SV2_OK ||
-            (rc = launch_bias_rows(txt_out, in->b_txt, dt, text_len, c.dim, stream)) != SV2_OK)
+        if ((rc = gemm_rows_bias(stream, dt, text_len, c.text_channels, c.dim, x, in->w_txt, in->b_txt, txt_out)) !=
+            SV2_OK)
             return rc;
     }
     // timestep: sinusoid, proj_in + silu, proj_hid + silu, proj_out (:360-392), fp32
     if ((rc = launch_sinusoid(sin, timestep, c.sinusoidal_dim, stream)) != SV2_OK ||
-        (rc = gemm_rows(stream, SV2_F32, 1, c.sinusoidal_dim, c.dim, sin, in->w_tin, h1)) != SV2_OK ||
-        (rc = launch_bias_act(h1, in->b_tin, SV2_F32, 1, c.dim, 1, stream)) != SV2_OK ||
-        (rc = gemm_rows(stream, SV2_F32, 1, c.dim, c.dim, h1, in->w_thid, h2)) != SV2_OK ||
-        (rc = launch_bias_act(h2, in->b_thid, SV2_F32, 1, c.dim, 1, stream)) != SV2_OK ||
-        (rc = gemm_rows(stream, SV2_F32, 1, c.dim, c.embedding_dim, h2, in->w_tout, emb)) != SV2_OK ||
-        (rc = launch_bias_rows(emb, in->b_tout, SV2_F32, 1, c.embedding_dim, stream)) != SV2_OK)
+        (rc = gemm_rows_bias(stream, SV2_F32, 1, c.sinusoidal_dim, c.dim, sin, in->w_tin, in->b_tin, h1)) != SV2_OK ||
+        (rc = launch_bias_act(h1, nullptr, SV2_F32, 1, c.dim, 1, stream)) != SV2_OK ||
+        (rc = gemm_rows_bias(stream, SV2_F32, 1, c.dim, c.dim, h1, in->w_thid, in->b_thid, h2)) != SV2_OK ||
+        (rc = launch_bias_act(h2, nullptr, SV2_F32, 1, c.dim, 1, stream)) != SV2_OK ||
+        (rc = gemm_rows_bias(stream, SV2_F32, 1, c.dim, c.embedding_dim, h2, in->w_tout, in->b_tout, emb)) != SV2_OK)
         return rc;
     return SV2_OK;
 }
@@ -562,8 +561,7 @@ int sv2_dit_output_forward(sv2_dit_output* o, const void* vid, const float* emb,
     if ((rc = launch_ada_table(emb, o->scale, nullptr, 0, c.dim, table, stream)) != SV2_OK ||
         (rc = launch_rmsnorm_table(vid, normed, dt, Lp, c.dim, c.norm_eps, table, o->shift, o->norm, 1, stream)) !=
             SV2_OK ||
-        (rc = gemm_rows(stream, dt, Lp, c.dim, P, normed, o->w_proj, projected)) != SV2_OK ||
-        (rc = launch_bias_rows(projected, o->b_proj, dt, Lp, P, stream)) != SV2_OK ||
+        (rc = gemm_rows_bias(stream, dt, Lp, c.dim, P, normed, o->w_proj, o->b_proj, projected)) != SV2_OK ||
         (rc = launch_unpatchify(projected, output, dt, frames, height, width, c.output_channels, channel_major,
                                 stream)) != SV2_OK)
         return rc;

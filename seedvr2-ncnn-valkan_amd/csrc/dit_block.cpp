@@ -13,6 +13,7 @@
 
 using sv2::gemm_mfma;
 using sv2::gemm_rows;
+using sv2::gemm_rows_bias;
 using sv2::kGemmResidual;
 using sv2::kGemmStore;
 using sv2::kGemmSwiGLU;
@@ -225,6 +226,9 @@ sv2_attn_args attention_args(const sv2_block* b, int text_len)
     a.rope_npos = b->rope_npos;
     a.qkv_dtype = b->dtype;
     a.out_dtype = b->dtype;
+    // the fp32 compute mode is the parity mode: the attention in the
+    // reference's own order and rounding
+    a.exact = b->dtype == SV2_F32 ? 1 : 0;
     const DevBranch& tb = b->cfg.shared_weights ? b->vid : b->txt;
     a.gamma_q_vid = b->vid.norm_q;
     a.gamma_k_vid = b->vid.norm_k;
@@ -627,13 +631,20 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     auto capture = [&](float* dst, const void* src, int rows, int cols) {
         return dst ? launch_to_f32(dst, src, dt, static_cast<long long>(rows) * cols, stream) : SV2_OK;
     };
-    // the projection before the gate: proj_out + bias, in fp32
+    // the projection before the gate: proj_out + bias, in fp32 (bias NULL:
+    // the product already holds it)
     auto capture_projected = [&](float* dst, const void* src, const float* bias, int rows) {
         if (!dst)
             return SV2_OK;
         const int r = launch_to_f32(dst, src, dt, static_cast<long long>(rows) * D, stream);
-        return r != SV2_OK ? r : launch_bias_rows(dst, bias, SV2_F32, rows, D, stream);
+        return (r != SV2_OK || !bias) ? r : launch_bias_rows(dst, bias, SV2_F32, rows, D, stream);
     };
+    // fp32: the proj_out bias enters the product's double sum before its one
+    // rounding, as in the InnerProduct; fp16: the gated residual pass adds it
+    const float* vbias_in_product = dt == SV2_F32 ? vb.b_proj : nullptr;
+    const float* vbias_in_residual = dt == SV2_F32 ? nullptr : vb.b_proj;
+    const float* tbias_in_product = dt == SV2_F32 ? tb.b_proj : nullptr;
+    const float* tbias_in_residual = dt == SV2_F32 ? nullptr : tb.b_proj;
     if (dbg && (rc = capture(dbg->qkv_vid, qkv_v, Lv, 3 * D)) != SV2_OK)
         return rc;
     if (Lt > 0)
@@ -686,23 +697,23 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
         }
         if (rc == SV2_EUNSUPPORTED)
         {
-            if ((rc = gemm_rows(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v)) != SV2_OK)
+            if ((rc = gemm_rows_bias(stream, dt, Lv, D, D, att_v, vb.w_proj, vbias_in_product, p_v)) != SV2_OK)
                 return rc;
-            if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vb.b_proj, Lv)) != SV2_OK)
+            if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vbias_in_residual, Lv)) != SV2_OK)
                 return rc;
-            if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vb.b_proj, 0, stream)) != SV2_OK)
+            if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vbias_in_residual, 0, stream)) != SV2_OK)
                 return rc;
         }
     }
     if (Lt > 0)
     {
-        if ((rc = gemm_rows(stream, dt, Lt, D, D, att_t, tb.w_proj, p_t)) != SV2_OK)
+        if ((rc = gemm_rows_bias(stream, dt, Lt, D, D, att_t, tb.w_proj, tbias_in_product, p_t)) != SV2_OK)
             return rc;
-        if (dbg && (rc = capture_projected(dbg->projected_txt, p_t, tb.b_proj, Lt)) != SV2_OK)
+        if (dbg && (rc = capture_projected(dbg->projected_txt, p_t, tbias_in_residual, Lt)) != SV2_OK)
             return rc;
         // the last layer adds the plain residual (:1198-1209)
-        if ((rc = launch_residual_table(p_t, txt, dt, Lt, D, tab_ta, tb.b_proj, c.last_layer ? 1 : 0, stream)) !=
-            SV2_OK)
+        if ((rc = launch_residual_table(p_t, txt, dt, Lt, D, tab_ta, tbias_in_residual, c.last_layer ? 1 : 0,
+                                        stream)) != SV2_OK)
             return rc;
     }
     // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)

@@ -6,6 +6,7 @@
 #include "vec_io.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace sv2
 {
@@ -13,6 +14,30 @@ namespace
 {
 
 using namespace vec;
+
+// 1.f / std::sqrt(float(ss / n) + eps) as the reference evaluates it
+// (seedvr2_dit_block.cpp:770-782) from the double sum of squares: the
+// double quotient rounded to float, then a correctly rounded float sqrt and
+// divide (each formed in double and rounded once, which for float operands is
+// the correctly rounded float result).
+__device__ inline float reference_inv_rms(double ss, int n, float eps)
+{
+    const float mean = static_cast<float>(ss / static_cast<double>(n));
+    const float root = static_cast<float>(__builtin_sqrt(static_cast<double>(mean + eps)));
+    return static_cast<float>(1.0 / static_cast<double>(root));
+}
+
+// std::exp of a float as the fp32 parity mode evaluates it: correctly rounded
+// (exp in double, rounded once); the 16-bit modes use the single-precision
+// library exp.
+template <typename T>
+__device__ inline float exp_of(float x)
+{
+    if constexpr (std::is_same_v<T, F32>)
+        return static_cast<float>(exp(static_cast<double>(x)));
+    else
+        return expf(x);
+}
 
 // Most 8-element vectors one lane keeps in registers per row (dim <= 8*64*kMaxVec).
 constexpr int kMaxVec = 8;
@@ -169,7 +194,7 @@ __global__ __launch_bounds__(256) void rmsnorm_ada_kernel(const void* x, void* y
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1)
             ss += __shfl_xor(ss, m);
-        const float inv = 1.f / sqrtf(static_cast<float>(ss / dim) + eps);
+        const float inv = reference_inv_rms(ss, dim, eps);
 #pragma unroll
         for (int k = 0; k < kVec; k++)
         {
@@ -310,15 +335,15 @@ __global__ __launch_bounds__(256) void swiglu_kernel(void* gate, const void* val
 #pragma unroll
     for (int e = 0; e < 8; e++)
     {
-        const float den = 1.f + expf(-g[e]);
+        const float den = 1.f + exp_of<T>(-g[e]);
         g[e] = (g[e] / den) * v[e];
     }
     st8<T>(gate, i, g);
 }
 
 // y[r][c] += b[c] (the bias of an InnerProduct whose matrix product ran
-// without one), optionally followed by silu(v) = v / (1 + exp(-v)) (the time
-// MLP of the DiT input head, seedvr2_dit_input.cpp:377-388).
+// without one; none when b is NULL), optionally followed by silu(v) = v / (1 +
+// exp(-v)) (the time MLP of the DiT input head, seedvr2_dit_input.cpp:377-388).
 template <typename T>
 __global__ __launch_bounds__(256) void bias_rows_kernel(void* y, const float* b, long long count, int cols,
                                                         int silu)
@@ -333,9 +358,10 @@ __global__ __launch_bounds__(256) void bias_rows_kernel(void* y, const float* b,
 #pragma unroll
     for (int e = 0; e < 8; e++)
     {
-        a[e] += b[c0 + e];
+        if (b)
+            a[e] += b[c0 + e];
         if (silu)
-            a[e] = a[e] / (1.f + expf(-a[e]));
+            a[e] = a[e] / (1.f + exp_of<T>(-a[e]));
     }
     st8<T>(y, i, a);
 }

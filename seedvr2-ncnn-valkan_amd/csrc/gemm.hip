@@ -369,15 +369,10 @@ int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, cons
                          "inner product: needs in a multiple of 64 and out a multiple of 256 (SwiGLU: 128)");
     if (!x || !w || !y || (epi == kResidual && !residual) || (epi == kSwiGLU && !w2))
         return set_error(SV2_EINVAL, "inner product: null pointer");
-    static bool attr = false;
-    if (!attr)
-    {
-        const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f16_kernel),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-        if (err != hipSuccess)
-            return hip_error(err, "gemm_mfma: dynamic LDS attribute");
-        attr = true;
-    }
+    const int rc = set_dynamic_lds(reinterpret_cast<const void*>(&gemm_f16_kernel), kLds,
+                                   "gemm_mfma: dynamic LDS attribute");
+    if (rc != SV2_OK)
+        return rc;
     GemmArgs a;
     a.x = static_cast<const _Float16*>(x);
     a.w = static_cast<const _Float16*>(w);

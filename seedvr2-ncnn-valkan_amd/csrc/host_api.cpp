@@ -3,7 +3,10 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "sv2_internal.h"
@@ -107,6 +110,25 @@ int hip_error(hipError_t err, const char* what)
     char buffer[256];
     std::snprintf(buffer, sizeof(buffer), "%s: %s", what, hipGetErrorString(err));
     return set_error(SV2_EDEVICE, buffer);
+}
+
+int set_dynamic_lds(const void* kernel, int bytes, const char* what)
+{
+    static std::mutex lock;
+    static std::map<std::pair<const void*, int>, int> done; // (kernel, device) -> limit set
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess)
+        return hip_error(err, what);
+    std::lock_guard<std::mutex> guard(lock);
+    int& limit = done[std::make_pair(kernel, device)];
+    if (limit >= bytes)
+        return SV2_OK;
+    err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess)
+        return hip_error(err, what);
+    limit = bytes;
+    return SV2_OK;
 }
 
 int build_plan(const sv2_window_rule& rule, PlanArgs* plan)

@@ -102,6 +102,10 @@ __host__ __device__ inline float bf16_round(float value)
 // Thread-local error message plumbing for the C ABI.
 int set_error(int code, const std::string& message);
 int hip_error(hipError_t err, const char* what);
+// Raises a kernel's dynamic LDS limit to at least `bytes` on the current
+// device.  The attribute is per device; it is set once per (kernel, device)
+// and size, under a lock, not on every launch.
+int set_dynamic_lds(const void* kernel, int bytes, const char* what);
 
 // Builds the closed-form plan; returns SV2_OK or an error code.
 int build_plan(const sv2_window_rule& rule, PlanArgs* plan);
@@ -127,11 +131,19 @@ int launch_residual_table(void* x, const void* residual, int dtype, int rows, in
                           const float* bias, int mode, hipStream_t stream);
 
 // y[rows, out] = x[rows, in] W^T, W [out][in] row-major (an InnerProduct
-// without its bias), in dtype (SV2_F32 or SV2_F16) with fp32 accumulation;
-// enqueued on `stream`.  fp16 runs on hipBLASLt (the first product of a shape
-// times the library's candidate kernels and synchronises the stream once),
-// fp32 on rocBLAS.
+// without its bias), in dtype (SV2_F32 or SV2_F16); enqueued on `stream`.
+// fp16 runs on hipBLASLt with fp32 accumulation (the first product of a
+// shape times the library's candidate kernels and synchronises the stream
+// once); fp32 on gemm_f32_exact.
 int gemm_rows(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y);
+// The same with the InnerProduct's bias (may be NULL): fp32 adds it to the
+// double sum before the one rounding; fp16 adds it in a pass after the product.
+int gemm_rows_bias(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w,
+                   const float* bias, void* y);
+// fp32 y = float(sum_i double(x_i) double(w_i) + double(bias)): products added
+// in increasing i, one rounding (gemm_exact.hip); bias may be NULL.
+int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x, const float* w, const float* bias,
+                   float* y);
 // fp16 only: y = gate[c] * (x W^T)[r][c] + residual[r][c] (+ bias[c] when
 // bias is not null), the gated residual of seedvr2_dit_block.cpp:807-825 in
 // the product's epilogue (fp32, one rounding to fp16); -2 when hipBLASLt has

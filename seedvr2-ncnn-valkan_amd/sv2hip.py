@@ -64,6 +64,7 @@ EXPORTS = [
     "sv2_dit_forward",
     "sv2_dit_destroy",
     "sv2_inner_product_f16",
+    "sv2_inner_product_f32",
     "sv2_euler_timesteps",
     "sv2_condition_ratio",
     "sv2_make_condition",
@@ -117,6 +118,7 @@ class AttnArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("debug_pre", ctypes.c_void_p),
+        ("exact", ctypes.c_int),
     ]
 
 
@@ -289,6 +291,8 @@ def load() -> ctypes.CDLL:
     lib.sv2_dit_destroy.restype = None
     lib.sv2_inner_product_f16.argtypes = [vp, vp, vp, vp, i, i, i, i, vp, vp, vp, vp]
     lib.sv2_inner_product_f16.restype = i
+    lib.sv2_inner_product_f32.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    lib.sv2_inner_product_f32.restype = i
     i64 = ctypes.c_int64
     lib.sv2_euler_timesteps.argtypes = [i, vp]
     lib.sv2_euler_timesteps.restype = i
@@ -377,8 +381,9 @@ class WindowAttention:
     configuration and launches sv2_window_attention on torch tensors."""
 
     def __init__(self, r: WindowRule, heads: int, text_len: int, *, eps=1e-5, qk_norm=True,
-                 rope_mode=ROPE_REFERENCE, freqs=None, theta=10000.0, device="cuda"):
+                 rope_mode=ROPE_REFERENCE, freqs=None, theta=10000.0, device="cuda", exact=False):
         import torch
+        self.exact = bool(exact)
         self.rule = r
         self.heads = heads
         self.text_len = text_len
@@ -418,6 +423,7 @@ class WindowAttention:
         a.txt_out = None if txt_out is None else txt_out.data_ptr()
         a.out_dtype = torch_dtype_code(vid_out)
         a.debug_pre = None if debug_pre is None else debug_pre.data_ptr()
+        a.exact = int(self.exact)
         return a
 
     def workspace_bytes(self, a: AttnArgs) -> int:
@@ -915,6 +921,21 @@ class EulerSampler:
 
 
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
+
+
+def inner_product_f32(x, w, y, bias=None, stream=None):
+    """y = float(sum_i double(x_i) double(w_i) + double(bias)) (sv2_inner_product_f32):
+    x fp32 [rows, in], w fp32 [out, in], y fp32 [rows, out], bias fp32 [out]."""
+    import torch
+    rows, k = x.shape
+    out = w.shape[0]
+    for name, t, shape in (("x", x, (rows, k)), ("w", w, (out, k)), ("y", y, (rows, out))):
+        if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"inner_product_f32: {name} must be a contiguous fp32 {shape}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != out):
+        raise ValueError("inner_product_f32: bias must be fp32 [out]")
+    check(load().sv2_inner_product_f32(_ptr(x), _ptr(w), _ptr(bias), _ptr(y), rows, k, out, _stream(stream)),
+          "sv2_inner_product_f32")
 
 
 def inner_product_f16(x, w, y, epilogue=EPI_STORE, w_value=None, bias=None, gate=None, residual=None,

@@ -50,7 +50,7 @@ def report(gpu: np.ndarray, ref: np.ndarray, gpu_pre=None, ref_pre=None) -> dict
     assert gpu.shape == ref.shape, (gpu.shape, ref.shape)
     out = {"n": int(gpu.size), "finite": bool(np.isfinite(gpu).all())}
     if gpu.size == 0:
-        out.update(max_abs=0.0, mean_abs=0.0, flips=0, over_tol_not_flip=0)
+        out.update(max_abs=0.0, mean_abs=0.0, flips=0, flip_frac=0.0, over_tol_not_flip=0)
         return out
     d = np.abs(gpu - ref)
     ulp = bf16_ulp(np.maximum(np.abs(gpu), np.abs(ref)))
@@ -59,6 +59,7 @@ def report(gpu: np.ndarray, ref: np.ndarray, gpu_pre=None, ref_pre=None) -> dict
     out["max_abs"] = float(d.max())
     out["mean_abs"] = float(d.mean())
     out["flips"] = int(flip.sum())
+    out["flip_frac"] = float(flip.mean())
     out["over_tol_not_flip"] = int((over & ~flip).sum())
     if gpu_pre is not None:
         dp = np.abs(np.asarray(gpu_pre, np.float64) - np.asarray(ref_pre, np.float64))

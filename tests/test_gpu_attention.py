@@ -29,6 +29,18 @@ def test_single_layer_2x16x30_unshifted_no_norm_no_rope(hip, orc, device):
           qk_norm=False, rope_mode=2, in_dtype="f32", out_dtype="f32", seed=1)
 
 
+@pytest.mark.parametrize("shifted", [False, True], ids=["unshifted", "shifted"])
+def test_single_layer_2x16x30_fp32_norm_rope_flip_rate(hip, orc, device, shifted):
+    # the fp32 parity mode at the config-2 shape: P enters P*V as three bf16
+    # terms against exact bf16 V, so the pre-rounding values are fp32-class
+    # and a bf16 rounding flip against the oracle is rare (< 0.1%; fp16 P flips
+    # about 8% of the elements)
+    rep_v, _ = _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=20, shifted=shifted, wt=2, wh=8, ww=10,
+                     qk_norm=True, rope_mode=0, in_dtype="f32", out_dtype="f32", seed=6 + shifted)
+    assert rep_v["flips"] <= 1e-3 * rep_v["n"], rep_v
+    assert rep_v["pre_max_abs"] <= 1e-5, rep_v
+
+
 def test_single_layer_2x16x30_fp16_shifted_norm_rope(hip, orc, device):
     # fp16 layer with QK-norm and RoPE, shifted (0,4,5) ragged windows (12)
     _case(hip, orc, device, T=2, H=16, W=30, Lt=L_TXT, heads=20, shifted=True, wt=2, wh=8, ww=10,
@@ -93,18 +105,26 @@ def test_index_map_bitexact(hip, orc, device):
         assert np.array_equal(out.cpu().numpy(), np.array(ref, dtype=np.int32))
 
 
-@pytest.mark.parametrize("rope_mode,in_dtype", [(0, "f16"), (1, "f32"), (2, "bf16")])
+@pytest.mark.parametrize("rope_mode,in_dtype", [(0, "f16"), (0, "f32"), (1, "f32"), (2, "bf16"), (0, "bf16")])
 def test_prologue_matches_oracle(hip, orc, device, rope_mode, in_dtype):
     """q/k/v after norm, rotation and bf16 rounding, through the same device
     code the attention kernel runs.  The RoPE table holds the host C library's
-    cosf/sinf and multiplies and adds are unfused as in the reference, so the
-    only source of difference is the per-head sum of squares, which the device
-    accumulates in fp32 where the reference uses double: an element may then
-    round to the neighbouring bf16 value (one ulp) — rare — and where the
-    rotation cancels (a*c - b*s near 0) the tiny result can move by a few of
-    its own ulps, bounded here by 1e-6 absolute on O(1) data.  v is compared as
-    the fp16 operand the kernel feeds the P*V MFMA: fp16 of the bf16 value,
-    exact except in fp16's subnormal range (|v| < 2^-14), where the kernel's
+    cosf/sinf, exactly the reference's values.
+    fp32 and bf16 inputs (the exact prologue): double sum of squares, float of
+    its mean, correctly rounded fp32 sqrt and divide, unfused products, as the
+    reference evaluates them; q and k are bit-identical to the oracle's (the
+    double sums run in another order, which changes the float mean only when
+    the sum lies within ~2^-50 of a rounding boundary: a handful of elements
+    at most is allowed).
+    fp16 inputs (the fast prologue): fp32 sum of squares, the hardware
+    reciprocal square root and one product fused into each RoPE add; an
+    element may then round to the neighbouring bf16 value (one ulp) — rare —
+    and where the rotation cancels (a*c - b*s near 0) the tiny result can move
+    by a few of its own ulps, bounded here by 1e-6 absolute on O(1) data.
+    v is compared as
+    the operand the kernel feeds the P*V MFMA.  fp32 and bf16 inputs: the bf16
+    value itself, bit for bit.  fp16 inputs: fp16 of the bf16 value, exact
+    except in fp16's subnormal range (|v| < 2^-14), where the kernel's
     conversion rounds toward zero (at most one fp16 subnormal step, 2^-24)."""
     import torch
     T, H, W, Lt, heads = 2, 16, 30, L_TXT, 4
@@ -126,7 +146,8 @@ def test_prologue_matches_oracle(hip, orc, device, rope_mode, in_dtype):
     attn.prologue(torch.from_numpy(vid).to(device, tdt), torch.from_numpy(txt).to(device, tdt),
                   [torch.from_numpy(g).to(device) for g in gam], *outs)
     torch.cuda.synchronize()
-    expect = {"q": caps["q"], "k": caps["k"], "v": caps["v"].astype(np.float16).astype(np.float32)}
+    v_expect = caps["v"].astype(np.float16).astype(np.float32) if in_dtype == "f16" else caps["v"]
+    expect = {"q": caps["q"], "k": caps["k"], "v": v_expect}
     for name, o in zip("qkv", outs):
         g = o.cpu().numpy()
         r = expect[name]
@@ -135,10 +156,15 @@ def test_prologue_matches_oracle(hip, orc, device, rope_mode, in_dtype):
         frac = differ.mean()
         print(f"  {name}: {int(differ.sum())} of {g.size} differ", flush=True)
         if name == "v":
+            if in_dtype != "f16":
+                assert not differ.any()
+                continue
             tiny = np.abs(r) < 2.0 ** -14
             assert not (differ & ~tiny).any()
             assert (np.abs(g[differ].astype(np.float64) - r[differ]) <= 2.0 ** -24).all()
             continue
+        if in_dtype != "f16":
+            assert int(differ.sum()) <= 4, f"{name}: {int(differ.sum())} elements differ in the exact prologue"
         assert frac <= 2e-3, f"{name}: {frac:.2e} of the elements differ"
         if differ.any():
             d = np.abs(g[differ].astype(np.float64) - r[differ])

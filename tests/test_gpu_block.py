@@ -17,12 +17,16 @@ tags), small random blocks over every layer variant, the loader for each
 weight record type, and the full-size block at 480x256x5 (960 video + 58
 text tokens, dim 2560, 20 heads, MLP hidden 6912, windows 2x8x10).
 
-At full size the bf16 rounding of the attention outputs (which the
-reference applies, seedvr2_dit_block.cpp:1074) flips a few percent of the
-elements by one bf16 ulp relative to the oracle, and the MLP amplifies those
-differences past 2e-3 at some elements of outputs of magnitude ~20.  The
-full-size and stage tests therefore gate each stage separately on the GPU's
-own stage input (check_stages) and the whole block on the reference's NRMSE.
+The full-size and stage tests also gate each stage separately on the GPU's
+own stage input (check_stages).  In the fp32 mode the attention carries P*V
+at fp32-class precision (P as three bf16 terms against exact bf16 V), so the
+bf16 rounding of the attention outputs (which the reference applies,
+seedvr2_dit_block.cpp:1074) lands on the oracle's side of a rounding boundary
+for all but a few elements in 10^4, and the whole block is gated end to end at
+max-abs 2e-3, mean-abs 2e-4 and NRMSE 2e-3.  In the fp16 mode (P in fp16, a
+few percent of one-ulp flips that the MLP amplifies on outputs of magnitude
+~20) the end-to-end gate is the reference's block gate, NRMSE <= 2e-3
+(tools/test_seedvr2_dit_ncnn.py:248).
 """
 from __future__ import annotations
 
@@ -261,9 +265,9 @@ def check_stages(hip, orc, blk, oblk, vid, txt, emb, T, H, W, device, what):
       attention  the windowed attention from the GPU's qkv (:870-1091); every
                  element within 2e-3 or a bf16 rounding flip of the output
       tail       proj + gates + MLPs from the GPU's attention outputs (:1180-1260)
-    End to end the differences of the attention's bf16 rounding flips travel
-    through the projections and the MLP, so the end-to-end comparison uses the
-    reference's block gate (NRMSE <= 2e-3)."""
+    End to end: fp32 mode within max-abs 2e-3, mean-abs 2e-4 and NRMSE 2e-3;
+    fp16 mode (whose attention rounding flips travel through the projections
+    and the MLP) within the reference's block gate, NRMSE <= 2e-3."""
     from parity import assert_parity, bf16_ulp, report
 
     strict = blk.dtype == hip.F32
@@ -290,8 +294,11 @@ def check_stages(hip, orc, blk, oblk, vid, txt, emb, T, H, W, device, what):
     else:
         stage_gate(reps["attention_vid"], f"{what} attention_vid", False)
         stage_gate(reps["attention_txt"], f"{what} attention_txt", False)
+    print(f"[{what}] attention_vid flips: {att_v['flips']} of {att_v['n']} ({att_v['flip_frac']:.2e})", flush=True)
     for k in ("end_to_end_vid", "end_to_end_txt"):
         stage_gate(reps[k], f"{what} {k}", False)
+        if strict:
+            stage_gate(reps[k], f"{what} {k}", True)
     return reps
 
 

@@ -102,11 +102,15 @@ def test_input_head(hip, orc, device, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_output_head(hip, orc, device, dtype):
+@pytest.mark.parametrize("grid", [(2, 4, 6), (3, 37, 37)], ids=["48rows", "4107rows"])
+def test_output_head(hip, orc, device, dtype, grid):
+    # 4107 rows: the RMSNorm * gamma + ada of the head on the 16-rows-per-
+    # workgroup instance (launches of >= 4096 rows) with a ragged last group
     code = hip.F32 if dtype == "f32" else hip.F16
-    print(f"[output head] {dtype}", flush=True)
+    print(f"[output head] {dtype} grid={grid}", flush=True)
     rng = np.random.default_rng(42)
-    dim, T, h, w = 2560, 2, 4, 6
+    dim = 2560
+    T, h, w = grid
     wts = nf.random_output_weights(rng, dim)
     vid = rng.standard_normal((T * h * w, dim), dtype=np.float32) * 3
     if code == hip.F16:

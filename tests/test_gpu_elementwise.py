@@ -12,7 +12,8 @@ expf differs from glibc's by an ulp); in fp16/bf16 the oracle runs on the
 same rounded inputs and the GPU output is within one ulp of the output dtype
 of the oracle's fp32 result.  Shapes: a DiT block at 480x256x5 (960 video +
 58 text rows, width 2560, MLP hidden 6912), rows that are not a multiple of
-the 4 rows a workgroup handles, and the widest row the kernel supports.
+the rows a workgroup handles (4, or 16 for launches of 4096 rows and more)
+and the widest row the kernel supports.
 """
 from __future__ import annotations
 
@@ -51,7 +52,10 @@ def dev(a, dtype, device):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
-@pytest.mark.parametrize("rows,dim", [(1018, 2560), (3, 2560), (5, 4096), (7, 8)])
+@pytest.mark.parametrize("rows,dim", [(1018, 2560), (3, 2560), (5, 4096), (7, 8),
+                                      # 16 rows per workgroup (launches of >= 4096 rows,
+                                      # every 720p layer) with a ragged last workgroup
+                                      (4099, 2560), (4096 + 16 * 3 + 5, 4096)])
 @pytest.mark.parametrize("slot,has_ada", [(0, True), (3, True), (0, False)])
 def test_rmsnorm_ada(hip, orc, device, dtype, rows, dim, slot, has_ada):
     print(f"[rmsnorm_ada] rows={rows} dim={dim} slot={slot} ada={has_ada} {dtype}", flush=True)

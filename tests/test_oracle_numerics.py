@@ -54,6 +54,28 @@ def test_bf16_ties_go_to_even(orc):
     assert np.isinf(orc.bf16(np.float32(3.4028235e38)))  # rounds past max bf16 to inf
 
 
+def test_expf_is_correctly_rounded_and_within_an_ulp_of_libm(orc):
+    """orc_expf, the oracle's std::exp(float) (softmax and silu), equals exp
+    in float64 rounded once to float32 (closed form), and differs from the host
+    libm's expf (the function the reference calls) by at most one ulp."""
+    import ctypes
+    import ctypes.util
+    rng = np.random.default_rng(7)
+    x = np.concatenate([rng.uniform(-40.0, 8.0, 20000), [0.0, -0.0, -1e-30, 1e-30, -87.0, 88.0, -104.0]])
+    x = x.astype(np.float32)
+    lib = orc.load()
+    got = np.array([lib.orc_expf(ctypes.c_float(v)) for v in x], dtype=np.float32)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.argtypes = [ctypes.c_float]
+    libm.expf.restype = ctypes.c_float
+    host = np.array([libm.expf(ctypes.c_float(v)) for v in x], dtype=np.float32)
+    ulps = np.abs(host.view(np.int32).astype(np.int64) - got.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1
+    assert (ulps > 0).mean() < 5e-3
+
+
 # ------------------------------------------------------------------ attention
 
 def _textbook(vid_qkv, txt_qkv, T, H, W, heads, windows, scale=HD ** -0.5):
