@@ -35,9 +35,16 @@
  *   orc_inner_product   y = W x + b in float64 (summation order of ncnn's
  *                       InnerProduct is not available here: parity unpinned
  *                       for GEMM summation order, values pinned by closed form)
- *   orc_block_forward   composition of the above; parity unpinned against
- *                       the reference block itself (no stored golden outputs
- *                       exist in the reference and ncnn is absent)
+ *   orc_block_forward   a float64 numpy statement of the block from the model's
+ *                       definitions with its own window plan, on weights
+ *                       designed so that a wrong branch, modulation slot or
+ *                       residual source fails (each planted and shown to
+ *                       fail); the algebra's identities bit for bit (W_out = 0
+ *                       leaves the gated projection plus the input; zero
+ *                       projections return the inputs); one window over the
+ *                       grid equals global joint attention
+ *   dit_forward (oracle.py) input head -> blocks -> output head against the
+ *                       same numpy statement with numpy heads
  *   orc_dit_input_forward, orc_dit_output_forward
  *                       patchify / unpatchify against an einops-style numpy
  *                       reshape, the sinusoid and time MLP against a float64
