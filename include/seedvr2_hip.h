@@ -155,6 +155,17 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args);
  * element is rounded to bf16 as the reference rounds it (:1074). */
 int sv2_window_attention(const sv2_attn_args* args, void* stream);
 
+/* Device.  sv2_window_attention for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it has no counterpart in the reference.  args->workspace
+ * and workspace_bytes are ignored: the scratch is a static device array of
+ * the library, 48 MiB per device (the 720p x 21f workload needs 43.7 MB), held
+ * until the process ends.  Calls whose sv2_window_attention_workspace exceeds
+ * it, and the exact mode, return SV2_EUNSUPPORTED.  Calls that overlap on one
+ * device share the array and race; calls on one stream are ordered.
+ * Allocates nothing (no hipMalloc / hipFree). */
+int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream);
+
 /* Device.  Debug/test entry: the prologue alone.  Writes q, k, v after
  * normalisation, rotation and bf16 rounding, fp32, each [sum_w S_w, heads*128]
  * in window-sequence order; the same device code the attention kernel runs

@@ -39,7 +39,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 namespace sv2
 {
@@ -2175,6 +2178,48 @@ int launch_exact(const AttnParams& p, const Workspace& w, char* base, int rope_m
 }
 
 } // namespace
+
+// Scratch of the no-allocation entry point (sv2_window_attention_no_alloc):
+// the per-window bf16 text partials and the prepared text q, k, v^T of one
+// attention call.  48 MiB covers the 720p x 21f workload (144 windows x 58
+// text tokens x 2560 channels of partials, 43.7 MB in all).  Each device that
+// loads the library holds its own copy until the process ends.  Every byte a
+// call reads is written earlier in the same call (all text rows of every
+// window and head, the whole prepared text), so nothing is cleared between
+// calls; calls that overlap on one device share it and race.
+constexpr int64_t kStaticScratchBytes = int64_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace
+{
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the array's name in host code is a host-side stand-in, not a
+// device address).
+int static_scratch_address(void** out)
+{
+    static std::mutex lock;
+    static std::map<int, void*> address;
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess)
+        return hip_error(err, "attention (no alloc): hipGetDevice");
+    std::lock_guard<std::mutex> guard(lock);
+    auto it = address.find(device);
+    if (it == address.end())
+    {
+        void* ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr)
+            return hip_error(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                             "attention (no alloc): address of the static scratch");
+        it = address.emplace(device, ptr).first;
+    }
+    *out = it->second;
+    return SV2_OK;
+}
+
+} // namespace
 } // namespace sv2
 
 extern "C" {
@@ -2229,6 +2274,34 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
             return hip_error(err, "text_window_reduce_kernel launch");
     }
     return SV2_OK;
+}
+
+int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream_ptr)
+{
+    using namespace sv2;
+    if (!args)
+        return set_error(SV2_EINVAL, "attention (no alloc): null args");
+    if (args->exact)
+        return set_error(SV2_EUNSUPPORTED,
+                         "attention (no alloc): the exact mode's window-sequence buffers exceed the static scratch");
+    const int64_t need = sv2_window_attention_workspace(args);
+    if (need < 0)
+        return static_cast<int>(need);
+    if (need > kStaticScratchBytes)
+    {
+        char msg[160];
+        std::snprintf(msg, sizeof(msg), "attention (no alloc): needs %lld bytes of scratch, the static scratch holds %lld",
+                      static_cast<long long>(need), static_cast<long long>(kStaticScratchBytes));
+        return set_error(SV2_EUNSUPPORTED, msg);
+    }
+    void* ptr = nullptr;
+    const int rc = static_scratch_address(&ptr);
+    if (rc != SV2_OK)
+        return rc;
+    sv2_attn_args a = *args;
+    a.workspace = ptr;
+    a.workspace_bytes = static_cast<size_t>(kStaticScratchBytes);
+    return sv2_window_attention(&a, stream_ptr);
 }
 
 int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float* v_out, void* stream_ptr)

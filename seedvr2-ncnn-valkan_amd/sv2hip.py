@@ -32,6 +32,7 @@ EXPORTS = [
     "sv2_rope_positions_needed",
     "sv2_window_attention_workspace",
     "sv2_window_attention",
+    "sv2_window_attention_no_alloc",
     "sv2_qk_prologue",
     "sv2_rmsnorm_ada",
     "sv2_ada_residual",
@@ -221,6 +222,8 @@ def load() -> ctypes.CDLL:
     lib.sv2_window_attention_workspace.restype = ctypes.c_int64
     lib.sv2_window_attention.argtypes = [ctypes.POINTER(AttnArgs), vp]
     lib.sv2_window_attention.restype = i
+    lib.sv2_window_attention_no_alloc.argtypes = [ctypes.POINTER(AttnArgs), vp]
+    lib.sv2_window_attention_no_alloc.restype = i
     lib.sv2_qk_prologue.argtypes = [ctypes.POINTER(AttnArgs), vp, vp, vp, vp]
     lib.sv2_qk_prologue.restype = i
     lib.sv2_rmsnorm_ada.argtypes = [vp, vp, i, i, i, ctypes.c_float, vp, vp, vp, i, i, vp]
@@ -442,6 +445,13 @@ class WindowAttention:
         a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
         self._bind_workspace(a, vid_qkv.device)
         check(load().sv2_window_attention(ctypes.byref(a), _stream(stream)), "sv2_window_attention")
+
+    def run_no_alloc(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
+        """The same attention through sv2_window_attention_no_alloc (the
+        library's static scratch; no workspace)."""
+        a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
+        check(load().sv2_window_attention_no_alloc(ctypes.byref(a), _stream(stream)),
+              "sv2_window_attention_no_alloc")
 
     def prologue(self, vid_qkv, txt_qkv, gammas, q_out, k_out, v_out, stream=None):
         a = self.args(vid_qkv, txt_qkv, gammas, q_out, None)
