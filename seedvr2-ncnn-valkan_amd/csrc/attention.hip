@@ -256,8 +256,8 @@ __device__ inline void store2<BF16>(void* base, long long offset, float a, float
 struct LdsLayout
 {
     int k;       // [3][64 rows][16 slots] x 16 B: key tiles, swizzled; bf16 after the prologue
-    int vraw;    // [2] x 16 KB: raw value tiles (video: [64 keys][16 chunks]; text: V^T slots)
-    int vt;      // [2][128 rows][64 keys] fp16: transposed value tiles, swizzled
+    int vraw;    // [2] x 16 KB: fetched value tiles, rows by 32-dim quarters (vq_offset)
+    int vt;      // [2][128 rows][64 keys]: transposed value tiles in the P*V operand type, swizzled
     int rows;    // int2 [vmax]: global video row, packed local (t | y << 10 | x << 20)
     int rope;    // float2 [rope_rows][24]: cos/sin rows t..., y..., x... of the window
     int gamma;   // float [2][128]: q, k gammas of the video branch
@@ -292,7 +292,7 @@ struct AttnParams
     float* dbg_pre;         // optional [sum S][D]
     uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
-    uint16_t* txt_vt;       // [heads][128][text_pad] P*V operand type, prepared and transposed
+    uint16_t* txt_vt;       // [heads][text_pad][128] P*V operand type, prepared
     int ordered;            // windows dispatched in the order of `order` (else in plan order)
     int exact;              // the reference-order fp64 kernel (fp32 inputs)
     long long seq_rows;     // sum over windows of S_w (window-sequence rows)
@@ -515,15 +515,19 @@ __device__ inline int k_slot_offset(int r, int c)
     return (c >> 3) * 8192 + r * 128 + (((c & 7) ^ ((r >> 1) & 7)) << 4);
 }
 
-// Byte offset of chunk c of row r in a raw value tile (same halves, no swizzle).
-__device__ inline int vraw_offset(int r, int c)
+// Byte offset of chunk c (dims 8c..8c+7) of key row r in a fetched value
+// tile: four 4 KB quarters (dims 32q..32q+31), 64 bytes per row within a
+// quarter.  The transposing reads of the V^T transpose (below) touch eight
+// rows of one quarter, 64 bytes each: every bank at most twice per wave and
+// once per half-wave, with no swizzle.
+__device__ inline int vq_offset(int r, int c)
 {
-    return (c >> 3) * 8192 + r * 128 + ((c & 7) << 4);
+    return (c >> 2) * 4096 + r * 64 + ((c & 3) << 4);
 }
 
 // Swizzled offset (in halfs) of key group `grp` (8 keys, 0..7) in row d of the
-// transposed value tile; spreads both the 16-byte reads of 8 consecutive rows
-// and the scattered writes of rows 8 apart over the banks.
+// transposed value tile; spreads the 16-byte operand reads of 8 consecutive
+// rows and the 16-byte writes of 16 consecutive rows over the banks.
 __device__ inline int vt_offset(int d, int grp)
 {
     return d * kVtStride + ((grp ^ ((d ^ (d >> 3)) & 7)) << 3);
@@ -547,6 +551,26 @@ __device__ inline uint32_t v_pair_operand(float a, float b)
         return __builtin_bit_cast(uint32_t, bf16_pair_as_f16(a, b));
     else
         return bf16_pair_bits(a, b);
+}
+
+// Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0) in the
+// P*V operand type of input type TI.
+template <typename TI>
+__device__ inline void store_vt_pair(char* vt, int r, int d0, const float v0[8], const float v1[8])
+{
+    uint16_t* t = reinterpret_cast<uint16_t*>(vt);
+    const int key = 2 * r;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        *reinterpret_cast<uint32_t*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = v_pair_operand<TI>(v0[e], v1[e]);
+}
+
+// Eight values of v rounded to bf16, in the P*V operand type of input type TI.
+template <typename TI>
+__device__ inline uint4 v_operand8(const float x[8])
+{
+    return make_uint4(v_pair_operand<TI>(x[0], x[1]), v_pair_operand<TI>(x[2], x[3]),
+                      v_pair_operand<TI>(x[4], x[5]), v_pair_operand<TI>(x[6], x[7]));
 }
 
 // A P*V operand element back in fp32 (for the prologue debug captures).
@@ -842,8 +866,8 @@ __device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const Ke
 
 // Text tokens: q/k prologue with the text branch's gammas and positions
 // (l, l, l) in the reference RoPE mode (text is not rotated in the absolute
-// mode), v rounded to bf16 and stored in the P*V operand type, transposed; zero padding up to
-// text_pad so masked keys multiply finite values.
+// mode), v rounded to bf16 and stored in the P*V operand type, [heads][text_pad][128]
+// with zero rows up to text_pad so masked keys multiply finite values.
 template <typename TI, int RM>
 __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
 {
@@ -912,16 +936,10 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
         *reinterpret_cast<uint4*>(p.txt_q + o) = qb;
         *reinterpret_cast<uint4*>(p.txt_k + o) = kb;
     }
-    // +0.0 is the all-zero pattern in fp16 and bf16 alike
-    uint16_t* vt = p.txt_vt;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2)
-    {
-        const uint32_t h = valid ? v_pair_operand<TI>(v[e], v[e + 1]) : 0u;
-        const long long base = (static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l;
-        vt[base] = static_cast<uint16_t>(h & 0xffffu);
-        vt[base + p.text_pad] = static_cast<uint16_t>(h >> 16);
-    }
+    // rows past text_len are zero (+0.0 is the all-zero pattern in fp16 and
+    // bf16 alike): masked keys then multiply finite values
+    *reinterpret_cast<uint4*>(p.txt_vt + (static_cast<long long>(head) * p.text_pad + l) * kHeadDim + d0) =
+        valid ? v_operand8<TI>(v) : make_uint4(0u, 0u, 0u, 0u);
 }
 
 // ---------------------------------------------------------------- key/value tiles
@@ -953,9 +971,10 @@ __device__ inline char* vt_tile(char* smem, const AttnParams& p, int kb)
 // wave-instruction at a time (the lane order fixes where each 16-byte chunk
 // lands).  Waves 0-7 fetch the key tile, wave w rows 8w..8w+7, one half (64
 // dims) per instruction, lane l taking row 8w + l / 8; waves 8-11 fetch the
-// value tile, wave 8+v rows 16v..16v+15 in four instructions.  Each wave
-// prepares exactly the rows it fetched, so no barrier separates the fetch
-// from the prologue.  Rows past the end of a ragged tile repeat the last
+// value tile, wave 8+v rows 16v..16v+15, one 32-dim quarter per instruction,
+// lane l taking row 16v + l / 4 (text value rows come prepared from the
+// workspace in the same layout).  Each wave prepares exactly the chunks it
+// fetched, so no barrier separates the fetch from the prologue.  Rows past the end of a ragged tile repeat the last
 // valid row: their scores are masked and their values multiply p = 0.
 // Fetches per lane and tile: 2 (key waves), 4 (value waves).
 template <typename TI>
@@ -981,34 +1000,21 @@ __device__ inline void dma_tile(const AttnParams& p, const Geometry& gm, const S
             dma16(krow + 8 * (8 * i + ksl), kt + i * 8192 + 8 * wave * 128);
         return;
     }
-    char* vr = vraw_tile(smem, p, kb);
+    // value rows: instruction q writes LDS bytes q * 4096 + 1024 v + 16 lane,
+    // i.e. chunk 4q + (lane & 3) of row 16v + lane / 4 (vq_offset)
+    char* vt = vraw_tile(smem, p, kb);
     const int v = wave - 8;
+    const int r = 16 * v + (lane >> 2);
+    const uint16_t* vrow;
     if (kb < gm.ntb)
-    {
-        // V^T slots: instruction q covers rows d = 8q .. 8q+7 of the transposed tile
+        vrow = p.txt_vt + (static_cast<long long>(head) * p.text_pad + kb * kBlockN + r) * kHeadDim;
+    else
+        vrow = static_cast<const uint16_t*>(p.vid_qkv) +
+               static_cast<long long>(s.rows[min((kb - gm.ntb) * kBlockN + r, gm.vlen - 1)].x) * p.row_stride +
+               2LL * p.dim + head * kHeadDim;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-        {
-            const int q = 4 * v + i;
-            const int d = 8 * q + (lane >> 3);
-            const int grp = sl ^ ((d ^ (d >> 3)) & 7);
-            dma16(p.txt_vt + (static_cast<long long>(head) * kHeadDim + d) * p.text_pad + kb * kBlockN + 8 * grp,
-                  vr + q * 1024);
-        }
-        return;
-    }
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-    {
-        const int r = 16 * v + 8 * b + (lane >> 3);
-        const uint16_t* vrow = static_cast<const uint16_t*>(p.vid_qkv) +
-                               static_cast<long long>(s.rows[min((kb - gm.ntb) * kBlockN + r, gm.vlen - 1)].x) *
-                                   p.row_stride +
-                               2LL * p.dim + head * kHeadDim;
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-            dma16(vrow + 8 * (8 * h + sl), vr + h * 8192 + (16 * v + 8 * b) * 128);
-    }
+    for (int q = 0; q < 4; q++)
+        dma16(vrow + 8 * (4 * q + (lane & 3)), vt + q * 4096 + 1024 * v);
 }
 
 // Waits until this lane's fetches of the older of the (at most) two tiles in
@@ -1023,23 +1029,32 @@ __device__ inline void wait_tile_fetch(int wave, bool newer_in_flight)
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt4);
 }
 
-// Writes the transposed value items of keys 2r, 2r+1 (8 dims at d0) in the
-// P*V operand type of input type TI.
-template <typename TI>
-__device__ inline void store_vt_pair(char* vt, int r, int d0, const float v0[8], const float v1[8])
+// Eight keys of one dim from a fetched value tile with two transposing LDS
+// reads (ds_read_b64_tr_b16).  Within each 16-lane group such a read hands
+// lane i element i % 4 of the 8-byte pieces addressed by group lanes
+// i / 4 + 4 j, j = 0..3; when group lane k addresses key row r0 + k / 4 at
+// dims d0 + 4 (k % 4), lane i receives keys r0 .. r0 + 3 of dim d0 + i.  The
+// second read is four rows (256 bytes) further.
+__device__ inline uint4 v_keys8_tr(const char* vr, int off)
 {
-    uint16_t* t = reinterpret_cast<uint16_t*>(vt);
-    const int key = 2 * r;
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        *reinterpret_cast<uint32_t*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) = v_pair_operand<TI>(v0[e], v1[e]);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vr + off));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vr + off + 256));
+    const uint2 a = __builtin_bit_cast(uint2, lo);
+    const uint2 b = __builtin_bit_cast(uint2, hi);
+    return make_uint4(a.x, a.y, b.x, b.y);
 }
 
 // 16-bit inputs: the prologue of tile kb, run by the waves that fetched it
-// (after their own fetches have landed).  Video: waves 0-7 run the k
-// prologue (RMSNorm * gamma, RoPE, bf16) in place, waves 8-11 round v to bf16
-// and write it transposed into the V^T tile.  Text (prepared in the
-// workspace): waves 8-11 copy the V^T slots to the V^T tile.
+// (after their own fetches have landed), so no barrier separates the fetch
+// from the prologue.  Video: waves 0-7 run the k prologue (RMSNorm * gamma,
+// RoPE, bf16) in place.  Waves 8-11 write the V^T tile from the rows they
+// fetched: wave 8+v's 16-lane groups read the 8-key columns of key groups 2v,
+// 2v+1 (16 dims per group and read) with transposing reads, round fp16 values
+// to bf16 (bf16 inputs and the prepared text rows are rounded already;
+// rounding them again changes nothing) and store each column as one 16-byte
+// chunk.
 template <typename TI, int RM>
 __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, const Staged& s, const RopeBase& rb,
                                     char* smem, int kb, int wave, int lane)
@@ -1067,30 +1082,26 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
         }
         return;
     }
-    char* vt = vt_tile(smem, p, kb);
     const char* vr = vraw_tile(smem, p, kb);
-    const int v = wave - 8;
-    if (kb < gm.ntb)
-    {
+    char* vt = vt_tile(smem, p, kb);
+    const int q = lane >> 4;
+    const int i = lane & 15;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+    for (int it = 0; it < 4; it++)
+    {
+        // key groups 2v, 2v+1 (the rows this wave fetched) x 8 blocks of 16 dims
+        const int blk = 4 * it + q;
+        const int db = blk & 7;
+        const int grp = 2 * (wave - 8) + (blk >> 3);
+        uint4 u = v_keys8_tr(vr, vq_offset(8 * grp + (i >> 2), 2 * db + ((i & 3) >> 1)) + 8 * (i & 1));
+        if constexpr (TI::kPTerms == 1)
         {
-            const int off = (4 * v + i) * 1024 + lane * 16;
-            *reinterpret_cast<uint4*>(vt + off) = *reinterpret_cast<const uint4*>(vr + off);
+            float x[8];
+            uint4 raw[1] = {u};
+            raw8_to_float<TI>(raw, x);
+            u = v_operand8<TI>(x);
         }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-    {
-        const int r = 8 * v + 4 * i + (lane >> 4); // keys 2r, 2r+1 (rows 16v..16v+15 of the raw tile)
-        uint4 a[1] = {*reinterpret_cast<const uint4*>(vr + vraw_offset(2 * r, chunk))};
-        uint4 b[1] = {*reinterpret_cast<const uint4*>(vr + vraw_offset(2 * r + 1, chunk))};
-        float v0[8];
-        float v1[8];
-        raw8_to_float<TI>(a, v0);
-        raw8_to_float<TI>(b, v1);
-        store_vt_pair<TI>(vt, r, d0, v0, v1);
+        *reinterpret_cast<uint4*>(vt + 2 * vt_offset(16 * db + i, grp)) = u;
     }
 }
 
@@ -1118,14 +1129,14 @@ __device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry
             *reinterpret_cast<uint4*>(kt + k_slot_offset(rr, chunk)) =
                 *reinterpret_cast<const uint4*>(p.txt_k + (kbase + l) * kHeadDim + d0);
         }
-        const long long vbase = static_cast<long long>(head) * kHeadDim;
+        // the prepared text rows (bf16 bits), transposed: keys 2r, 2r+1
+        const uint16_t* vs = p.txt_vt + (static_cast<long long>(head) * p.text_pad + base + 2 * r) * kHeadDim + d0;
+        uint16_t* t = reinterpret_cast<uint16_t*>(vt);
+        const int key = 2 * r;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-        {
-            const int item = tid + kLoaderThreads * i; // row d = item >> 3, key group item & 7
-            *reinterpret_cast<uint4*>(vt + 2 * vt_offset(item >> 3, item & 7)) =
-                *reinterpret_cast<const uint4*>(p.txt_vt + (vbase + (item >> 3)) * p.text_pad + base + (item & 7) * 8);
-        }
+        for (int e = 0; e < 8; e++)
+            *reinterpret_cast<uint32_t*>(&t[vt_offset(d0 + e, key >> 3) + (key & 7)]) =
+                static_cast<uint32_t>(vs[e]) | (static_cast<uint32_t>(vs[e + kHeadDim]) << 16);
         return;
     }
     const int base = (kb - gm.ntb) * kBlockN;
@@ -1715,13 +1726,12 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         {
             const int l = jc - box.vlen;
             const uint16_t* ks = p.txt_k + (static_cast<long long>(head) * p.text_len + l) * kHeadDim + d0;
-            const uint16_t* vs = p.txt_vt;
+            const uint16_t* vs = p.txt_vt + (static_cast<long long>(head) * p.text_pad + l) * kHeadDim + d0;
 #pragma unroll
             for (int e = 0; e < 8; e++)
             {
                 k_out[o + e] = __builtin_bit_cast(float, static_cast<uint32_t>(ks[e]) << 16);
-                v_out[o + e] =
-                    v_operand_value<TI>(vs[(static_cast<long long>(head) * kHeadDim + d0 + e) * p.text_pad + l]);
+                v_out[o + e] = v_operand_value<TI>(vs[e]);
             }
         }
     }
@@ -1929,25 +1939,27 @@ int align16(int v)
     return (v + 15) & ~15;
 }
 
-// LDS of the attention kernel for a plan: key/value tiles plus the staged
-// row table, RoPE rows and gammas of the largest window.
-LdsLayout lds_layout(int vmax, int rope_rows, bool dma)
+// LDS of the attention kernel for a plan: the staged row table of the largest
+// window, then the key/value tiles, RoPE rows and gammas; after the tile loop
+// the 16-bit epilogue stages its outputs over those last three (the row table
+// is still read there).
+LdsLayout lds_layout(int vmax, int rope_rows)
 {
     LdsLayout l;
     int off = 0;
+    l.rows = off;
+    off = align16(off + vmax * 8);
     l.k = off;
     off += 3 * kTileBytes;
     l.vraw = off;
-    off += dma ? 2 * kTileBytes : 0;
+    off += 2 * kTileBytes;
     l.vt = off;
     off += 2 * kTileBytes;
-    l.rows = off;
-    off = align16(off + vmax * 8);
     l.rope = off;
     off = align16(off + rope_rows * kRopePairSlots * 8);
     l.gamma = off;
     off += 2 * kHeadDim * 4;
-    l.total = off;
+    l.total = std::max(off, l.k + kWaves * 32 * kEpiStride);
     return l;
 }
 
@@ -2033,8 +2045,7 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
     const int64_t qkv_elems = static_cast<int64_t>(a->rule.frames) * a->rule.height * a->rule.width * 3 * a->heads * kHeadDim;
     if (qkv_elems >= (int64_t(1) << 40))
         return set_error(SV2_EUNSUPPORTED, "attention: qkv tensor too large");
-    p->lds = lds_layout(vmax, rope_rows, a->qkv_dtype != SV2_F32);
-    static_assert(kWaves * 32 * kEpiStride <= 7 * kTileBytes, "epilogue staging must fit the tile buffers");
+    p->lds = lds_layout(vmax, rope_rows);
     if (p->lds.total > kMaxLds)
         return set_error(SV2_EUNSUPPORTED, "attention: the window's staged tables exceed the LDS of a CU");
     p->vid_qkv = a->vid_qkv;
