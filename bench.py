@@ -42,19 +42,67 @@ def plan_stats(shifted: bool):
     return wins, sizes, flops
 
 
+ATTENTION_SOURCE = REPO / "seedvr2-ncnn-valkan_amd" / "csrc" / "attention.hip"
+TRAFFIC_FILE = REPO / "profiles" / "window_attention_720p_traffic.json"
+
+
+def source_sha256(path: Path = ATTENTION_SOURCE) -> str:
+    import hashlib
+    return hashlib.sha256(path.read_bytes()).hexdigest()
+
+
+def measured_traffic():
+    """HBM bytes per attention launch from the committed FETCH_SIZE /
+    WRITE_SIZE measurement, used only when it measured this kernel source
+    (its attention_source_sha256 stamp); else None and the reason."""
+    if not TRAFFIC_FILE.exists():
+        return None, "no traffic measurement committed"
+    try:
+        tf = json.loads(TRAFFIC_FILE.read_text())
+    except ValueError:
+        return None, "traffic file does not parse"
+    if tf.get("attention_source_sha256") != source_sha256():
+        return None, "traffic file measured another attention kernel source"
+    return tf.get("hbm_bytes_per_launch"), "FETCH_SIZE/WRITE_SIZE of this kernel source, " + TRAFFIC_FILE.name
+
+
 def algorithmic_bytes(elem=2):
     tokens = T * H * W + L_TXT
     return tokens * 3 * HEADS * HD * elem + tokens * HEADS * HD * elem
 
 
+def host_cpu() -> dict:
+    """The host's core count (the cores this process may run on) and CPU model."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": nproc, "cpu_model": model, "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def cpu_baseline(target_s: float = 15.0):
     """The CPU oracle on the shifted 720p plan: video queries of a sample of
     windows plus the text queries of every window (the text output averages
-    over all windows).  Returns TFLOPS of the work actually done."""
+    over all windows).  Returns TFLOPS of the work actually done.
+
+    Threads: all cores this process may use, capped by OMP_NUM_THREADS (the
+    CPU share a GPU's host process is given, when set) and by the 20 heads the
+    oracle's attention parallelises over."""
     import oracle
     from parity import reference_freqs
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    threads = max(1, min(threads, 16, HEADS))
+    host = host_cpu()
+    threads = host["nproc"]
+    if host["omp_num_threads"]:
+        threads = min(threads, int(host["omp_num_threads"]))
+    threads = max(1, min(threads, HEADS))
     wins, sizes, _ = plan_stats(True)
     rng = np.random.default_rng(7)
     D = HEADS * HD
@@ -88,6 +136,9 @@ def cpu_baseline(target_s: float = 15.0):
         "value": work / dt / 1e12,
         "unit": "TFLOPS",
         "cores": threads,
+        "nproc": host["nproc"],
+        "cpu_model": host["cpu_model"],
+        "omp_num_threads": host["omp_num_threads"],
         "kind": "port",
         "sample": (f"CPU oracle (C restatement of the reference CPU layer, OpenMP over heads) on the "
                    f"shifted 720p plan: video queries of {k} of {len(wins)} windows + text queries of "
@@ -366,13 +417,7 @@ def main():
         }
     t_launch = float(np.mean(per_layer_ms)) * 1e-3
     achieved = B / t_launch / 1e9
-    traffic = None
-    tf = REPO / "profiles" / "window_attention_720p_traffic.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic, traffic_source = measured_traffic()
 
     result = {
         "metric": "window-attn TFLOPS & % fp16 MFMA peak; DiT step ms @720p×21f, 1 GPU",
@@ -406,6 +451,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
+            "kernel": "window_attention_kernel<F16, reference RoPE> (per layer: text prepare + attention + text reduce, "
+                      "timed with HIP events on the launch stream)",
         },
     }
     if args.dit_steps > 0:
