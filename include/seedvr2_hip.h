@@ -295,19 +295,28 @@ int sv2_block_forward(sv2_block* block, const void* vid, const void* txt, int te
 void sv2_block_destroy(sv2_block* block);
 
 /* Intermediate captures of one forward, fp32 device arrays (any may be NULL).
- * Replaces SeedVR2DiTBlockDebugTensors (seedvr2_dit_block.h:20-36) for the
- * fields the block itself produces: qkv, the attention outputs (bf16-rounded,
- * text averaged over windows; the inputs of proj_out), the projections
- * before the gate (:1188-1192) and the outputs. */
+ * Replaces SeedVR2DiTBlockDebugTensors (seedvr2_dit_block.h:20-36): its 14
+ * fields in the reference's row orders, plus the attention outputs as
+ * proj_out reads them.  S_sum = sum over the windows of (window video tokens
+ * + L_txt): the window-sequence rows (each window's video tokens t -> y -> x,
+ * then the text tokens), in plan order. */
 typedef struct sv2_block_debug {
     float* qkv_vid;       /* [L_v, 3*dim] */
     float* qkv_txt;       /* [L_txt, 3*dim] */
-    float* attention_vid; /* [L_v, dim] */
-    float* attention_txt; /* [L_txt, dim] */
-    float* projected_vid; /* [L_v, dim] */
+    float* attention_vid; /* [L_v, dim]: bf16-rounded attention outputs, the input of proj_out */
+    float* attention_txt; /* [L_txt, dim]: text outputs averaged over windows (:1081-1088) */
+    float* projected_vid; /* [L_v, dim]: proj_out + bias before the gate (:1188-1192) */
     float* projected_txt; /* [L_txt, dim] */
     float* output_vid;    /* [L_v, dim] */
     float* output_txt;    /* [L_txt, dim] */
+    float* norm_q_vid;    /* [L_v, dim]: q after RMSNorm * gamma, before RoPE (:908-918, :986-990) */
+    float* norm_q_txt;    /* [L_txt, dim] (:1007-1012) */
+    float* norm_k_vid;    /* [L_v, dim] */
+    float* norm_k_txt;    /* [L_txt, dim] */
+    float* attention_q;   /* [S_sum, dim]: q after norm, RoPE and bf16, window-sequence order (:1030-1043) */
+    float* attention_k;   /* [S_sum, dim] */
+    float* attention_v;   /* [S_sum, dim]: v rounded to bf16 (in the fp16 mode: as the fp16 operand) */
+    float* attention_output; /* [S_sum, dim]: each query's bf16-rounded output per window (:1074-1077) */
 } sv2_block_debug;
 
 /* Enables captures for the following forwards (NULL disables them), as

@@ -98,6 +98,8 @@ def load() -> ctypes.CDLL:
     lib.orc_window_attention.argtypes = [ctypes.POINTER(OrcAttnCfg), i, i, i, i, vp, vp, vp, vp,
                                          vp, vp, vp, vp, vp]
     lib.orc_window_attention.restype = i
+    lib.orc_qk_norms.argtypes = [ctypes.POINTER(OrcAttnCfg), i, i, vp, vp, vp, vp, vp, vp]
+    lib.orc_qk_norms.restype = i
     lib.orc_rmsnorm_rows.argtypes = [vp, i, i, ctypes.c_float]
     lib.orc_ada_input.argtypes = [vp, i, i, vp, vp, vp, i]
     lib.orc_ada_output_residual.argtypes = [vp, vp, i, i, vp, vp, i]
@@ -206,6 +208,25 @@ def window_attention(vid_qkv, txt_qkv, T, H, W, *, heads, head_dim=128, eps=1e-5
     if capture:
         return vid_out, txt_out, caps
     return vid_out, txt_out
+
+
+def qk_norms(vid_qkv, txt_qkv, *, heads, head_dim=128, eps=1e-5, qk_norm=True, gammas=None):
+    """q and k after RMSNorm * gamma, before RoPE (the reference's norm_q/k_vid
+    and norm_q/k_txt captures).  Returns (nq_vid, nk_vid, nq_txt, nk_txt)."""
+    vid_qkv, txt_qkv = _f32(vid_qkv), _f32(txt_qkv)
+    D = heads * head_dim
+    ones = np.ones(head_dim, dtype=np.float32)
+    g = [(_f32(x) if x is not None else ones) for x in (gammas or (None,) * 4)]
+    fr = np.zeros(21, dtype=np.float32)
+    cfg = OrcAttnCfg(heads, head_dim, eps, int(bool(qk_norm)), ROPE_NONE, _p(fr), 10000.0,
+                     _p(g[0]), _p(g[1]), _p(g[2]), _p(g[3]), 0, 0, 0, 0, 0)
+    Lv, Lt = vid_qkv.shape[0], txt_qkv.shape[0]
+    out = [np.zeros((Lv, D), np.float32), np.zeros((Lv, D), np.float32), np.zeros((Lt, D), np.float32),
+           np.zeros((Lt, D), np.float32)]
+    rc = load().orc_qk_norms(ctypes.byref(cfg), Lv, Lt, _p(vid_qkv), _p(txt_qkv), *[_p(o) for o in out])
+    if rc != 0:
+        raise RuntimeError(f"orc_qk_norms failed: {rc}")
+    return tuple(out)
 
 
 def rmsnorm_rows(x, eps):

@@ -144,11 +144,11 @@ static void make_rope_layout(const orc_attn_cfg* cfg, rope_layout* r)
     }
 }
 
-/* seedvr2_dit_block.cpp:942-974 (normalize_and_rotate): per-head RMSNorm with
- * a double sum, gamma, adjacent-pair rotation, then bf16 of every dim. */
-static void normalize_and_rotate(const float* source, const float* gamma, float* destination,
-                                 int head_dim, float eps, int qk_norm, const rope_layout* rope,
-                                 int rotate, const int positions[3])
+/* The per-head RMSNorm * gamma step of normalize_and_rotate
+ * (seedvr2_dit_block.cpp:947-951): a double sum, float mean, then x * inv * g.
+ * Without the q/k norm the values pass through. */
+static void normalize_head(const float* source, const float* gamma, float* destination, int head_dim, float eps,
+                           int qk_norm)
 {
     if (qk_norm)
     {
@@ -164,6 +164,15 @@ static void normalize_and_rotate(const float* source, const float* gamma, float*
         for (int d = 0; d < head_dim; d++)
             destination[d] = source[d];
     }
+}
+
+/* seedvr2_dit_block.cpp:942-974 (normalize_and_rotate): per-head RMSNorm with
+ * a double sum, gamma, adjacent-pair rotation, then bf16 of every dim. */
+static void normalize_and_rotate(const float* source, const float* gamma, float* destination,
+                                 int head_dim, float eps, int qk_norm, const rope_layout* rope,
+                                 int rotate, const int positions[3])
+{
+    normalize_head(source, gamma, destination, head_dim, eps, qk_norm);
     if (rotate)
     {
         for (int axis = 0; axis < 3; axis++)
@@ -181,6 +190,43 @@ static void normalize_and_rotate(const float* source, const float* gamma, float*
     }
     for (int d = 0; d < head_dim; d++)
         destination[d] = orc_bf16(destination[d]);
+}
+
+/* The debug captures norm_q/k_vid and norm_q/k_txt of the reference
+ * (seedvr2_dit_block.h:20-36, filled at :908-918 and :989-1016): q and k of
+ * every head after RMSNorm * gamma and before RoPE, video rows in grid order
+ * [Lv][dim], text rows [Lt][dim]; any output may be NULL. */
+int orc_qk_norms(const orc_attn_cfg* cfg, int Lv, int Lt, const float* vid_qkv, const float* txt_qkv,
+                 float* nq_vid, float* nk_vid, float* nq_txt, float* nk_txt)
+{
+    const int hd = cfg->head_dim;
+    const int dim = cfg->heads * hd;
+    if (Lv < 0 || Lt < 0)
+        return -1;
+    for (int head = 0; head < cfg->heads; head++)
+    {
+        for (int r = 0; r < Lv; r++)
+        {
+            const float* row = vid_qkv + (size_t)r * 3 * dim;
+            if (nq_vid)
+                normalize_head(row + head * hd, cfg->gq_vid, nq_vid + (size_t)r * dim + head * hd, hd, cfg->eps,
+                               cfg->qk_norm);
+            if (nk_vid)
+                normalize_head(row + dim + head * hd, cfg->gk_vid, nk_vid + (size_t)r * dim + head * hd, hd,
+                               cfg->eps, cfg->qk_norm);
+        }
+        for (int l = 0; l < Lt; l++)
+        {
+            const float* row = txt_qkv + (size_t)l * 3 * dim;
+            if (nq_txt)
+                normalize_head(row + head * hd, cfg->gq_txt, nq_txt + (size_t)l * dim + head * hd, hd, cfg->eps,
+                               cfg->qk_norm);
+            if (nk_txt)
+                normalize_head(row + dim + head * hd, cfg->gk_txt, nk_txt + (size_t)l * dim + head * hd, hd,
+                               cfg->eps, cfg->qk_norm);
+        }
+    }
+    return 0;
 }
 
 /* seedvr2_dit_block.cpp:870-1091 */

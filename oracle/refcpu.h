@@ -132,6 +132,12 @@ int orc_window_attention(const orc_attn_cfg* cfg, int T, int H, int W, int Lt,
                          float* cap_q, float* cap_k, float* cap_v, float* cap_pre,
                          const unsigned char* video_mask);
 
+/* q and k of every head after RMSNorm * gamma, before RoPE: the reference's
+ * norm_q/k_vid (grid row order) and norm_q/k_txt debug captures
+ * (seedvr2_dit_block.h:20-36, :908-918, :989-1016).  Outputs may be NULL. */
+int orc_qk_norms(const orc_attn_cfg* cfg, int Lv, int Lt, const float* vid_qkv, const float* txt_qkv,
+                 float* nq_vid, float* nk_vid, float* nq_txt, float* nk_txt);
+
 /* Token RMSNorm over the last dim, no gamma (seedvr2_dit_block.cpp:770-782). */
 void orc_rmsnorm_rows(float* x, int rows, int dim, float eps);
 

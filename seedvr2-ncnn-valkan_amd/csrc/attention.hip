@@ -293,6 +293,8 @@ struct AttnParams
     uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_vt;       // [heads][text_pad][128] P*V operand type, prepared
+    float* nq_txt;          // optional debug captures [text_len][D]: text q, k after the norm, before RoPE
+    float* nk_txt;
     int ordered;            // windows dispatched in the order of `order` (else in plan order)
     int exact;              // the reference-order fp64 kernel (fp32 inputs)
     long long seq_rows;     // sum over windows of S_w (window-sequence rows)
@@ -460,15 +462,23 @@ __device__ inline float2 rotate_unfused(float first, float second, float2 c)
 // y = x * inv * gamma, then the rotation of the 4 adjacent pairs of the 8
 // dims (seedvr2_dit_block.cpp:950-971): (a, b) -> (a c - b s, b c + a s).
 // cs(q) gives the (cos, sin) of pair q.  kExact: unfused products (the
-// reference's rounding); else one product fused into the add.
+// reference's rounding); else one product fused into the add.  norm_out (the
+// debug captures only): the 8 values after the norm, before the rotation.
 template <bool kRotate, bool kExact, typename CosSin>
-__device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, CosSin cs)
+__device__ inline void scale_rotate8(float x[8], const float* gamma8, float inv, bool norm, CosSin cs,
+                                     float* norm_out = nullptr)
 {
     if (norm)
     {
 #pragma unroll
         for (int e = 0; e < 8; e++)
             x[e] = x[e] * inv * gamma8[e];
+    }
+    if (norm_out)
+    {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            norm_out[e] = x[e];
     }
     if constexpr (kRotate)
     {
@@ -727,9 +737,11 @@ __device__ inline void query_load(const AttnParams& p, const Staged& s, const Wi
     }
 }
 
+// norm_out (the debug captures only): where dims 8g.. of the row's values
+// after the norm and before RoPE go (chunk c at norm_out + 16 c); video rows.
 template <typename TI, int RM>
 __device__ inline void query_finish(const AttnParams& p, const Staged& s, const WindowBox& box, int qrow, int g,
-                                    const QueryRaw<TI>& raw, bf16x8 qf[8])
+                                    const QueryRaw<TI>& raw, bf16x8 qf[8], float* norm_out = nullptr)
 {
     const bool is_video = qrow < box.vlen;
     if (!is_video)
@@ -789,7 +801,7 @@ __device__ inline void query_finish(const AttnParams& p, const Staged& s, const 
             const int ia = (axis_a == 0 ? base0 : (axis_a == 1 ? base1 : base2)) + slot_a;
             const int ib = (axis_b == 0 ? base0 : (axis_b == 1 ? base1 : base2)) + slot_b;
             return s.rope[g ? ib : ia];
-        });
+        }, norm_out ? norm_out + 16 * c : nullptr);
         qf[c] = __builtin_bit_cast(bf16x8, to_bf16x8(&x[8 * c]));
     }
 }
@@ -837,7 +849,7 @@ __device__ inline KeyRope key_rope(const RopeBase& rb, int d0)
 // gamma, RoPE, bf16 rounding.
 template <int RM, bool kExact>
 __device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const KeyRope& kr, float x[8], int d0,
-                                  uint32_t packed)
+                                  uint32_t packed, float* norm_out = nullptr)
 {
     float inv = 1.f;
     if (p.qk_norm)
@@ -858,7 +870,7 @@ __device__ inline uint4 key_chunk(const AttnParams& p, const Staged& s, const Ke
     scale_rotate8<RM != SV2_ROPE_NONE, kExact>(x, &s.gamma[kHeadDim + d0], inv, p.qk_norm != 0, [&](int q) {
         const int local = static_cast<int>((packed >> kr.shift[q]) & 1023u);
         return s.rope[kr.off[q] + local * kRopePairSlots];
-    });
+    }, norm_out);
     return to_bf16x8(x);
 }
 
@@ -924,8 +936,9 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
         }
     }
     constexpr bool rotate = RM == SV2_ROPE_REFERENCE;
-    scale_rotate8<rotate, TI::kExact>(q, gq, iq, p.qk_norm != 0, cs);
-    scale_rotate8<rotate, TI::kExact>(k, gk, ik, p.qk_norm != 0, cs);
+    const long long cap = (static_cast<long long>(valid ? l : 0) * p.dim) + static_cast<long long>(head) * kHeadDim + d0;
+    scale_rotate8<rotate, TI::kExact>(q, gq, iq, p.qk_norm != 0, cs, (p.nq_txt && valid) ? p.nq_txt + cap : nullptr);
+    scale_rotate8<rotate, TI::kExact>(k, gk, ik, p.qk_norm != 0, cs, (p.nk_txt && valid) ? p.nk_txt + cap : nullptr);
     const uint4 qb = to_bf16x8(q);
     const uint4 kb = to_bf16x8(k);
     if (l >= p.text_pad)
@@ -1649,14 +1662,25 @@ __global__ __launch_bounds__(256) void text_window_reduce_kernel(const uint32_t*
     store2<TO>(out, 2 * i, a0 * inv_nw, a1 * inv_nw);
 }
 
+// Outputs of qk_prologue_kernel (each may be NULL): q, k, v after the
+// prologue in window-sequence order [sum S][D]; video q, k after the norm and
+// before RoPE in grid row order [T*H*W][D].
+struct PrologueOut
+{
+    float* q;
+    float* k;
+    float* v;
+    float* nq_vid;
+    float* nk_vid;
+};
+
 // Debug / test: q, k, v after the prologue, fp32, window-sequence order, from
 // the device functions the attention kernel runs: queries through the MFMA
 // operand-layout path, keys 16 lanes per row, values as the P*V operands;
 // text rows from the prepared workspace.  One workgroup (4 waves) per
 // (window, head, 32 rows).
 template <typename TI, int RM>
-__global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb, float* q_out, float* k_out,
-                                                          float* v_out)
+__global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb, PrologueOut out)
 {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int blk = blockIdx.x;
@@ -1683,14 +1707,17 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
         QueryRaw<TI> raw;
         query_load<TI>(p, s, box, head, min(j, seq - 1), g, raw);
         bf16x8 qf[8];
-        query_finish<TI, RM>(p, s, box, min(j, seq - 1), g, raw, qf);
-        if (j < seq)
+        float* nq = (out.nq_vid && j < box.vlen)
+                        ? out.nq_vid + static_cast<long long>(s.rows[j].x) * p.dim + q_col + 8 * g
+                        : nullptr;
+        query_finish<TI, RM>(p, s, box, min(j, seq - 1), g, raw, qf, nq);
+        if (j < seq && out.q)
         {
 #pragma unroll
             for (int c = 0; c < 8; c++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    q_out[(seq_base + j) * p.dim + q_col + 16 * c + 8 * g + e] = static_cast<float>(qf[c][e]);
+                    out.q[(seq_base + j) * p.dim + q_col + 16 * c + 8 * g + e] = static_cast<float>(qf[c][e]);
         }
     }
     const int d0 = (tid & 15) * 8;
@@ -1708,17 +1735,23 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
             float v[8];
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + p.dim + d0, k);
             load8<TI>(p.vid_qkv, static_cast<long long>(vr.x) * p.row_stride + q_col + 2LL * p.dim + d0, v);
-            const bf16x8 kb = __builtin_bit_cast(bf16x8, key_chunk<RM, TI::kExact>(p, s, kr, k, d0, static_cast<uint32_t>(vr.y)));
-            if (valid)
+            float* nk = (out.nk_vid && valid) ? out.nk_vid + static_cast<long long>(vr.x) * p.dim + q_col + d0 : nullptr;
+            const bf16x8 kb =
+                __builtin_bit_cast(bf16x8, key_chunk<RM, TI::kExact>(p, s, kr, k, d0, static_cast<uint32_t>(vr.y), nk));
+            if (valid && out.k)
+            {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    out.k[o + e] = static_cast<float>(kb[e]);
+            }
+            if (valid && out.v)
             {
 #pragma unroll
                 for (int e = 0; e < 8; e += 2)
                 {
                     const uint32_t h = v_pair_operand<TI>(v[e], v[e + 1]);
-                    k_out[o + e] = static_cast<float>(kb[e]);
-                    k_out[o + e + 1] = static_cast<float>(kb[e + 1]);
-                    v_out[o + e] = v_operand_value<TI>(static_cast<uint16_t>(h & 0xffffu));
-                    v_out[o + e + 1] = v_operand_value<TI>(static_cast<uint16_t>(h >> 16));
+                    out.v[o + e] = v_operand_value<TI>(static_cast<uint16_t>(h & 0xffffu));
+                    out.v[o + e + 1] = v_operand_value<TI>(static_cast<uint16_t>(h >> 16));
                 }
             }
         }
@@ -1730,8 +1763,10 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(AttnParams p, int nrb,
 #pragma unroll
             for (int e = 0; e < 8; e++)
             {
-                k_out[o + e] = __builtin_bit_cast(float, static_cast<uint32_t>(ks[e]) << 16);
-                v_out[o + e] = v_operand_value<TI>(vs[e]);
+                if (out.k)
+                    out.k[o + e] = __builtin_bit_cast(float, static_cast<uint32_t>(ks[e]) << 16);
+                if (out.v)
+                    out.v[o + e] = v_operand_value<TI>(vs[e]);
             }
         }
     }
@@ -2135,26 +2170,47 @@ void launch_reduce(const AttnParams& p, void* out, hipStream_t stream)
 }
 
 template <typename TI, int RM>
-int launch_prologue(const AttnParams& p, int nrb, float* q_out, float* k_out, float* v_out, hipStream_t stream)
+int launch_prologue(const AttnParams& p, int nrb, const PrologueOut& out, hipStream_t stream)
 {
     if (p.text_len > 0)
         launch_text_prepare<TI, RM>(p, stream);
     const unsigned grid = static_cast<unsigned>(p.plan.nwin) * p.heads * nrb;
-    hipLaunchKernelGGL((qk_prologue_kernel<TI, RM>), dim3(grid), dim3(256), p.lds.total, stream, p, nrb, q_out,
-                       k_out, v_out);
+    hipLaunchKernelGGL((qk_prologue_kernel<TI, RM>), dim3(grid), dim3(256), p.lds.total, stream, p, nrb, out);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "qk_prologue launch");
 }
 
 template <typename TI>
-int launch_prologue_rope(const AttnParams& p, int rope_mode, int nrb, float* q_out, float* k_out, float* v_out,
-                         hipStream_t stream)
+int launch_prologue_rope(const AttnParams& p, int rope_mode, int nrb, const PrologueOut& out, hipStream_t stream)
 {
     if (rope_mode == SV2_ROPE_REFERENCE)
-        return launch_prologue<TI, SV2_ROPE_REFERENCE>(p, nrb, q_out, k_out, v_out, stream);
+        return launch_prologue<TI, SV2_ROPE_REFERENCE>(p, nrb, out, stream);
     if (rope_mode == SV2_ROPE_ABSOLUTE)
-        return launch_prologue<TI, SV2_ROPE_ABSOLUTE>(p, nrb, q_out, k_out, v_out, stream);
-    return launch_prologue<TI, SV2_ROPE_NONE>(p, nrb, q_out, k_out, v_out, stream);
+        return launch_prologue<TI, SV2_ROPE_ABSOLUTE>(p, nrb, out, stream);
+    return launch_prologue<TI, SV2_ROPE_NONE>(p, nrb, out, stream);
+}
+
+// The prologue alone with any of its captures (PrologueOut, and the text
+// norms through p.nq_txt / p.nk_txt): the debug entry points.
+int run_prologue(const sv2_attn_args* args, const PrologueOut& out, float* nq_txt, float* nk_txt,
+                 hipStream_t stream)
+{
+    AttnParams p;
+    int smax = 0, vmax = 0, rope_rows = 0;
+    int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
+    if (rc != SV2_OK)
+        return rc;
+    if ((rc = bind_workspace(args, &p)) != SV2_OK)
+        return rc;
+    p.lds = lds_layout_staging(vmax, rope_rows);
+    p.nq_txt = nq_txt;
+    p.nk_txt = nk_txt;
+    const int nrb = (smax + 31) / 32;
+    if (args->qkv_dtype == SV2_F32)
+        return launch_prologue_rope<F32>(p, args->rope_mode, nrb, out, stream);
+    if (args->qkv_dtype == SV2_F16)
+        return launch_prologue_rope<F16>(p, args->rope_mode, nrb, out, stream);
+    return launch_prologue_rope<BF16>(p, args->rope_mode, nrb, out, stream);
 }
 
 // Exact mode: the prologue into the workspace's window-sequence buffers, then
@@ -2167,7 +2223,7 @@ int launch_exact(const AttnParams& p, const Workspace& w, char* base, int rope_m
     float* q = reinterpret_cast<float*>(base + w.seq_q);
     float* k = reinterpret_cast<float*>(base + w.seq_k);
     float* v = reinterpret_cast<float*>(base + w.seq_v);
-    int rc = launch_prologue_rope<F32>(ps, rope_mode, (smax + 31) / 32, q, k, v, stream);
+    int rc = launch_prologue_rope<F32>(ps, rope_mode, (smax + 31) / 32, PrologueOut{q, k, v, nullptr, nullptr}, stream);
     if (rc != SV2_OK)
         return rc;
     const int sstride = (smax + 3) & ~3;
@@ -2231,6 +2287,15 @@ int static_scratch_address(void** out)
 }
 
 } // namespace
+
+int attention_captures(const sv2_attn_args* args, float* q, float* k, float* v, float* nq_vid, float* nk_vid,
+                       float* nq_txt, float* nk_txt, hipStream_t stream)
+{
+    if (!q && !k && !v && !nq_vid && !nk_vid && !nq_txt && !nk_txt)
+        return SV2_OK;
+    return run_prologue(args, PrologueOut{q, k, v, nq_vid, nk_vid}, nq_txt, nk_txt, stream);
+}
+
 } // namespace sv2
 
 extern "C" {
@@ -2318,23 +2383,12 @@ int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream_ptr)
 int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float* v_out, void* stream_ptr)
 {
     using namespace sv2;
-    AttnParams p;
-    int smax = 0, vmax = 0, rope_rows = 0;
-    int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
-    if (rc != SV2_OK)
-        return rc;
+    if (!args)
+        return set_error(SV2_EINVAL, "qk_prologue: null args");
     if (!q_out || !k_out || !v_out)
         return set_error(SV2_EINVAL, "qk_prologue: null output pointer");
-    if ((rc = bind_workspace(args, &p)) != SV2_OK)
-        return rc;
-    p.lds = lds_layout_staging(vmax, rope_rows);
-    const int nrb = (smax + 31) / 32;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    if (args->qkv_dtype == SV2_F32)
-        return launch_prologue_rope<F32>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
-    if (args->qkv_dtype == SV2_F16)
-        return launch_prologue_rope<F16>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
-    return launch_prologue_rope<BF16>(p, args->rope_mode, nrb, q_out, k_out, v_out, stream);
+    return run_prologue(args, PrologueOut{q_out, k_out, v_out, nullptr, nullptr}, nullptr, nullptr,
+                        static_cast<hipStream_t>(stream_ptr));
 }
 
 int sv2_window_index_map(const sv2_window_rule* rule, int32_t* out, void* stream_ptr)

@@ -665,8 +665,29 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     a.txt_out = Lt > 0 ? att_t : nullptr;
     a.workspace = ws + w.attn;
     a.workspace_bytes = w.total - w.attn;
+    if (dbg)
+    {
+        // the prologue's captures from this forward's own qkv: norm_q/k before
+        // RoPE, attention_q/k/v in window-sequence order (:908-918, :1030-1043)
+        if ((rc = sv2::attention_captures(&a, dbg->attention_q, dbg->attention_k, dbg->attention_v,
+                                          dbg->norm_q_vid, dbg->norm_k_vid, Lt > 0 ? dbg->norm_q_txt : nullptr,
+                                          Lt > 0 ? dbg->norm_k_txt : nullptr, stream)) != SV2_OK)
+            return rc;
+        a.debug_pre = dbg->attention_output;
+    }
     if ((rc = sv2_window_attention(&a, stream)) != SV2_OK)
         return rc;
+    if (dbg && dbg->attention_output)
+    {
+        // every query's output per window, rounded to bf16 where the kernel
+        // (and the reference, :1074) rounds it
+        const int nwin = sv2_window_plan(&a.rule, nullptr, 0);
+        if (nwin < 0)
+            return nwin;
+        const long long seq_rows = static_cast<long long>(Lv) + static_cast<long long>(nwin) * Lt;
+        if ((rc = sv2::launch_bf16_round(dbg->attention_output, seq_rows * D, stream)) != SV2_OK)
+            return rc;
+    }
     if (dbg && ((rc = capture(dbg->attention_vid, att_v, Lv, D)) != SV2_OK ||
                 (Lt > 0 && (rc = capture(dbg->attention_txt, att_t, Lt, D)) != SV2_OK)))
         return rc;

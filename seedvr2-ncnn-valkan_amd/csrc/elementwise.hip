@@ -378,6 +378,14 @@ __global__ __launch_bounds__(256) void to_f32_kernel(float* dst, const void* src
     st8<F32>(dst, i, a);
 }
 
+// x = bf16(x), round to nearest even on the bits (seedvr2_dit_block.cpp:68-79).
+__global__ __launch_bounds__(256) void bf16_round_kernel(float* x, long long count)
+{
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < count)
+        x[i] = bf16_round(x[i]);
+}
+
 bool dtype_ok(int t)
 {
     return t == SV2_F32 || t == SV2_F16 || t == SV2_BF16;
@@ -407,6 +415,18 @@ int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int 
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "bias_rows_kernel launch");
 }
+int launch_bf16_round(float* x, long long count, hipStream_t stream)
+{
+    if (count <= 0)
+        return SV2_OK;
+    const long long blocks = (count + 255) / 256;
+    if (blocks > 0x7fffffffLL)
+        return set_error(SV2_EUNSUPPORTED, "bf16_round: too many elements");
+    hipLaunchKernelGGL(bf16_round_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, x, count);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "bf16_round_kernel launch");
+}
+
 int launch_to_f32(float* dst, const void* src, int dtype, long long count, hipStream_t stream)
 {
     if (!dtype_ok(dtype) || count < 0 || count % 8 != 0)

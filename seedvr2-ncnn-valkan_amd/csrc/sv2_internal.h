@@ -107,6 +107,15 @@ int hip_error(hipError_t err, const char* what);
 // and size, under a lock, not on every launch.
 int set_dynamic_lds(const void* kernel, int bytes, const char* what);
 
+// The attention prologue's debug captures for these attention arguments
+// (each output may be NULL): q, k, v after the prologue in window-sequence
+// order [sum S][D]; q, k after the norm and before RoPE, video rows in grid
+// order [T*H*W][D] and text rows [L_txt][D].  Enqueued on `stream`.
+int attention_captures(const sv2_attn_args* args, float* q, float* k, float* v, float* nq_vid, float* nk_vid,
+                       float* nq_txt, float* nk_txt, hipStream_t stream);
+// Rounds count fp32 values to bf16 (nearest even) in place.
+int launch_bf16_round(float* x, long long count, hipStream_t stream);
+
 // Builds the closed-form plan; returns SV2_OK or an error code.
 int build_plan(const sv2_window_rule& rule, PlanArgs* plan);
 

@@ -163,7 +163,8 @@ class BlockBranch(ctypes.Structure):
 
 
 BLOCK_DEBUG_FIELDS = ("qkv_vid", "qkv_txt", "attention_vid", "attention_txt", "projected_vid", "projected_txt",
-                      "output_vid", "output_txt")
+                      "output_vid", "output_txt", "norm_q_vid", "norm_q_txt", "norm_k_vid", "norm_k_txt",
+                      "attention_q", "attention_k", "attention_v", "attention_output")
 
 
 class BlockDebug(ctypes.Structure):

@@ -402,3 +402,84 @@ def test_fused_needs_supported_dims(hip):
         hip.DitBlock.from_host(hip.block_config(dim=384, heads=3, mlp_hidden=512, shared_weights=1, fused_gemm=1), w,
                                hip.F16)
     assert err.value.code == hip.SV2_EUNSUPPORTED
+
+
+# ---- the debug captures (SeedVR2DiTBlockDebugTensors) ----------------------
+
+def _differing(a, b) -> int:
+    return int((np.ascontiguousarray(a, np.float32).view(np.uint32)
+                != np.ascontiguousarray(b, np.float32).view(np.uint32)).sum())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("variant", SMALL_VARIANTS[:4] + SMALL_VARIANTS[5:6],
+                         ids=[v[0] for v in SMALL_VARIANTS[:4] + SMALL_VARIANTS[5:6]])
+def test_debug_captures_match_the_oracle(hip, orc, device, variant, dtype):
+    """Every capture of the reference's debug struct (seedvr2_dit_block.h:20-36)
+    against the oracle's same quantity computed from the GPU's own qkv capture:
+    norm_q/k_vid/txt (q, k after RMSNorm * gamma, before RoPE, :908-918,
+    :986-1016), attention_q/k/v in window-sequence order (:1030-1043) and the
+    bf16-rounded per-window attention outputs (:1074-1077).  fp32 mode (the
+    reference's arithmetic): bit for bit.  fp16 mode: the fast prologue may
+    round a q/k element to the neighbouring bf16 value (2e-3 of the elements
+    at most), v is the fp16 operand of the bf16 value, outputs within the
+    attention gate."""
+    from parity import assert_parity, report
+    name, over, (T, H, W), L = variant
+    code = hip.F32 if dtype == "f32" else hip.F16
+    print(f"[debug captures] {name} {dtype}", flush=True)
+    dim, heads, hidden = 256, 2, 512
+    cfg = hip.block_config(dim=dim, heads=heads, mlp_hidden=hidden, **over)
+    rng = np.random.default_rng(13)
+    w = nf.random_weights(rng, dim, hidden, shared=bool(cfg.shared_weights))
+    vid = rng.standard_normal((T * H * W, dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    txt = rng.standard_normal((L, dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    emb = rng.standard_normal(6 * dim, dtype=np.float32)
+    plan = orc.make_windows(T, H, W, bool(cfg.shifted_window), cfg.window_t, cfg.window_h, cfg.window_w)
+    seq = sum((p[1] - p[0]) * (p[3] - p[2]) * (p[5] - p[4]) + L for p in plan)
+    Lv = T * H * W
+    shapes = {"qkv_vid": (Lv, 3 * dim), "qkv_txt": (L, 3 * dim), "norm_q_vid": (Lv, dim), "norm_k_vid": (Lv, dim),
+              "norm_q_txt": (L, dim), "norm_k_txt": (L, dim), "attention_q": (seq, dim), "attention_k": (seq, dim),
+              "attention_v": (seq, dim), "attention_output": (seq, dim)}
+    caps = {k: torch.full(s, float("nan"), device=device) for k, s in shapes.items()}
+    blk = hip.DitBlock.from_host(cfg, w, code)
+    try:
+        blk.set_debug(caps)
+        run_gpu(hip, blk, vid, txt, emb, T, H, W, device)
+        blk.set_debug(None)
+    finally:
+        blk.close()
+    g = {k: v.cpu().numpy() for k, v in caps.items()}
+    tb = w["vid"] if cfg.shared_weights else w["txt"]
+    gam = [w["vid"]["norm_q"], w["vid"]["norm_k"], tb["norm_q"], tb["norm_k"]]
+    nq_v, nk_v, nq_t, nk_t = orc.qk_norms(g["qkv_vid"], g["qkv_txt"], heads=heads, qk_norm=bool(cfg.qk_norm),
+                                          gammas=gam)
+    _, _, ref = orc.window_attention(g["qkv_vid"], g["qkv_txt"], T, H, W, heads=heads, qk_norm=bool(cfg.qk_norm),
+                                     rope_mode=cfg.rope_mode, freqs=w["freqs"], gammas=gam,
+                                     shifted=bool(cfg.shifted_window), wt=cfg.window_t, wh=cfg.window_h,
+                                     ww=cfg.window_w, capture=True)
+    pairs = {"norm_q_vid": nq_v, "norm_k_vid": nk_v, "norm_q_txt": nq_t, "norm_k_txt": nk_t,
+             "attention_q": ref["q"], "attention_k": ref["k"]}
+    for k, r in pairs.items():
+        nd = _differing(g[k], r)
+        print(f"  {k}: {nd} of {r.size} differ", flush=True)
+        assert np.isfinite(g[k]).all()
+        if dtype == "f32":
+            assert nd <= 2, k
+        elif k.startswith("norm"):
+            assert np.abs(g[k].astype(np.float64) - r).max() <= 4e-6 * max(1.0, float(np.abs(r).max())), k
+        else:
+            assert nd <= 2e-3 * r.size, k
+    v_ref = ref["v"] if dtype == "f32" else ref["v"].astype(np.float16).astype(np.float32)
+    nd = _differing(g["attention_v"], v_ref)
+    print(f"  attention_v: {nd} of {v_ref.size} differ", flush=True)
+    assert nd == 0 if dtype == "f32" else (np.abs(g["attention_v"] - v_ref) <= 2.0 ** -24).all()
+    out_ref = orc.bf16_array(ref["pre"])
+    if dtype == "f32":
+        nd = _differing(g["attention_output"], out_ref)
+        print(f"  attention_output: {nd} of {out_ref.size} differ", flush=True)
+        assert nd <= 2
+    else:
+        rep = report(g["attention_output"], out_ref)
+        print(f"  attention_output: {rep}", flush=True)
+        assert_parity(rep, "attention_output")

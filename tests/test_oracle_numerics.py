@@ -253,6 +253,25 @@ def test_rope_reference_leaves_dims_126_127_unrotated(orc):
 
 # ------------------------------------------------------------------ elementwise
 
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_qk_norms_closed_form(orc, qk_norm):
+    """orc_qk_norms (the reference's norm_q/k debug captures): per head
+    x / sqrt(mean(x^2) + eps) * gamma in float64, before any rotation; the
+    identity without the q/k norm; video and text rows take their own gammas."""
+    rng = np.random.default_rng(19)
+    heads, Lv, Lt = 3, 7, 4
+    D = heads * HD
+    vid = (rng.standard_normal((Lv, 3 * D)) * 2).astype(np.float32)
+    txt = (rng.standard_normal((Lt, 3 * D)) * 2).astype(np.float32)
+    gam = [rng.uniform(0.5, 1.5, HD).astype(np.float32) for _ in range(4)]
+    out = orc.qk_norms(vid, txt, heads=heads, qk_norm=qk_norm, gammas=gam)
+    for o, src, col, g in ((out[0], vid, 0, gam[0]), (out[1], vid, D, gam[1]), (out[2], txt, 0, gam[2]),
+                           (out[3], txt, D, gam[3])):
+        x = src[:, col:col + D].astype(np.float64).reshape(src.shape[0], heads, HD)
+        want = x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + 1e-5) * g if qk_norm else x
+        assert np.abs(o.reshape(want.shape) - want).max() <= 1e-6 * max(1.0, np.abs(want).max())
+
+
 def test_rmsnorm_closed_form(orc):
     rng = np.random.default_rng(20)
     x = (rng.standard_normal((7, 2560)) * 3).astype(np.float32)
