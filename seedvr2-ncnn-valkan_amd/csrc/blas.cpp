@@ -1,13 +1,16 @@
 // Matrix products of the InnerProduct layers.
 //
 // fp16 (the fast mode): hipBLASLt with fp32 accumulation.  The first product
-// of a shape on a device asks the library for its 16 best-ranked kernels that
-// need no workspace, times each on the caller's stream with the caller's
-// buffers and keeps the fastest for the rest of the process; that first call
-// therefore synchronises the stream once.  Without a workspace, products on
-// different streams share nothing.  The gated form carries the block's gated
-// residual in the library's epilogue (per-channel alpha, beta 1, optional
-// bias), planned per shape in the same way.
+// of a shape on a device plans it: the library's best-ranked kernel that needs
+// no workspace, kept for the rest of the process.  The choice depends on the
+// shape alone, so a shape is computed with the same kernel (and rounds the
+// same way) in every process, and planning neither runs nor synchronises
+// anything.  (Timing the library's 16 best-ranked kernels instead and keeping
+// the fastest changed the 720p DiT step by less than its run-to-run spread.)
+// Without a workspace, products on different streams share nothing.  The
+// gated form carries the block's gated residual in the library's epilogue
+// (per-channel alpha, beta 1, optional bias), planned per shape in the same
+// way.
 // fp32 (the parity mode): gemm_f32_exact (gemm_exact.hip), double
 // accumulation in the order of the CPU restatement, the bias added in double.
 #include <hipblaslt/hipblaslt.h>
@@ -80,8 +83,20 @@ struct Gated
     const float* bias = nullptr;
 };
 
-int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out, const void* x, const void* w,
-              void* y, const Gated* gated, LtPlan* plan)
+void destroy_plan(LtPlan* plan)
+{
+    if (plan->d)
+        hipblasLtMatrixLayoutDestroy(plan->d);
+    if (plan->b)
+        hipblasLtMatrixLayoutDestroy(plan->b);
+    if (plan->a)
+        hipblasLtMatrixLayoutDestroy(plan->a);
+    if (plan->desc)
+        hipblasLtMatmulDescDestroy(plan->desc);
+    *plan = LtPlan();
+}
+
+int describe(int rows, int in, int out, const Gated* gated, LtPlan* plan)
 {
     if (hipblasLtMatmulDescCreate(&plan->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
         return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmulDescCreate failed");
@@ -114,9 +129,27 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
         hipblasLtMatrixLayoutCreate(&plan->b, HIP_R_16F, in, rows, in) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&plan->d, HIP_R_16F, out, rows, out) != HIPBLAS_STATUS_SUCCESS)
         return set_error(SV2_EDEVICE, "gemm: hipBLASLt descriptor setup failed");
+    return SV2_OK;
+}
+
+// Plans one product shape: the library's best-ranked kernel that needs no
+// workspace.  The choice depends on the shape alone (no timing), so every
+// process computes a shape with the same kernel and the same rounding, and
+// planning never touches the stream.
+int make_plan(hipblasLtHandle_t h, int rows, int in, int out, const Gated* gated, LtPlan* plan)
+{
+    int rc = describe(rows, in, out, gated, plan);
+    if (rc != SV2_OK)
+    {
+        destroy_plan(plan);
+        return rc;
+    }
     hipblasLtMatmulPreference_t pref = nullptr;
     if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS)
+    {
+        destroy_plan(plan);
         return set_error(SV2_EDEVICE, "gemm: hipblasLtMatmulPreferenceCreate failed");
+    }
     const uint64_t no_workspace = 0;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
                                           sizeof(no_workspace));
@@ -126,44 +159,14 @@ int make_plan(hipblasLtHandle_t h, hipStream_t stream, int rows, int in, int out
     const hipblasStatus_t hs =
         hipblasLtMatmulAlgoGetHeuristic(h, plan->desc, plan->a, plan->b, plan->d, plan->d, pref, kCandidates, res, &got);
     hipblasLtMatmulPreferenceDestroy(pref);
-    if (hs != HIPBLAS_STATUS_SUCCESS || got <= 0)
-        return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no kernel for an fp16 product of this shape");
-    const float one = 1.f;
-    const float zero = 0.f;
-    const void* alpha = gated ? static_cast<const void*>(gated->gate) : &one;
-    const float* beta = gated ? &one : &zero;
-    const void* c = gated ? gated->residual : y;
-    hipEvent_t e0 = nullptr;
-    hipEvent_t e1 = nullptr;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
-        return set_error(SV2_EDEVICE, "gemm: hipEventCreate failed");
-    float best = -1.f;
-    for (int i = 0; i < got; i++)
-    {
-        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize != 0)
-            continue;
-        bool ok = hipblasLtMatmul(h, plan->desc, alpha, w, plan->a, x, plan->b, beta, c, plan->d, y, plan->d,
-                                  &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipEventRecord(e0, stream) == hipSuccess;
-        for (int r = 0; r < 3 && ok; r++)
-            ok = hipblasLtMatmul(h, plan->desc, alpha, w, plan->a, x, plan->b, beta, c, plan->d, y, plan->d,
-                                 &res[i].algo, nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
-        float ms = 0.f;
-        if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
-            continue;
-        if (best < 0.f || ms < best)
+    for (int i = 0; hs == HIPBLAS_STATUS_SUCCESS && i < got; i++)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0)
         {
-            best = ms;
             plan->algo = res[i].algo;
+            return SV2_OK;
         }
-    }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    if (best < 0.f)
-        return set_error(gated ? SV2_EUNSUPPORTED : SV2_EDEVICE,
-                         "gemm: no hipBLASLt kernel ran for an fp16 product of this shape");
-    return SV2_OK;
+    destroy_plan(plan);
+    return set_error(SV2_EUNSUPPORTED, "gemm: hipBLASLt has no workspace-free kernel for an fp16 product of this shape");
 }
 
 int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, void* y,
@@ -189,7 +192,7 @@ int gemm_f16(hipStream_t stream, int rows, int in, int out, const void* x, const
         if (it == plans.end())
         {
             LtPlan fresh;
-            if ((rc = make_plan(h, stream, rows, in, out, x, w, y, gated, &fresh)) != SV2_OK)
+            if ((rc = make_plan(h, rows, in, out, gated, &fresh)) != SV2_OK)
             {
                 if (gated && rc == SV2_EUNSUPPORTED)
                     unsupported.insert(key);
