@@ -294,6 +294,24 @@ int sv2_block_forward(sv2_block* block, const void* vid, const void* txt, int te
 
 void sv2_block_destroy(sv2_block* block);
 
+/* Host.  Rows of the window-sequence order at the current runtime shape:
+ * the sum over the windows of (window video tokens + text_len), the row
+ * count of the attention_q/k/v/output captures (seedvr2_dit_block.cpp:
+ * 1030-1043). */
+int64_t sv2_block_window_rows(const sv2_block* block, int text_len);
+
+/* Host buffers.  One block forward from and to host memory, as the layer's
+ * CPU forward over ncnn::Mat blobs (SeedVR2DiTBlock::forward,
+ * seedvr2_dit_block.cpp:1114-1267): vid [T*H*W, dim], txt [text_len, dim],
+ * emb [6*dim] and the outputs are fp32 host arrays, whatever the compute
+ * dtype.  host_debug (may be NULL): fp32 host arrays of the captures wanted
+ * for this call (the sizes of sv2_block_debug).  Stages everything through
+ * device memory the block keeps (grown on demand), runs on the null stream
+ * and returns when the outputs are on the host.  This is the entry point of
+ * the ncnn layer adapter; device callers use sv2_block_forward. */
+int sv2_block_forward_host(sv2_block* block, const float* vid, const float* txt, int text_len, const float* emb,
+                           float* vid_out, float* txt_out, const struct sv2_block_debug* host_debug);
+
 /* Intermediate captures of one forward, fp32 device arrays (any may be NULL).
  * Replaces SeedVR2DiTBlockDebugTensors (seedvr2_dit_block.h:20-36): its 14
  * fields in the reference's row orders, plus the attention outputs as
@@ -421,7 +439,10 @@ typedef struct sv2_dit sv2_dit;
 /* Loads a whole exported DiT from `model_dir` (SeedVR2DiT::load, dit.cpp:
  * 120-174, resident mode): seedvr2_dit_input.ncnn.{param,bin},
  * seedvr2_dit_block_NN.ncnn.{param,bin} for NN = 00..31 and
- * seedvr2_dit_output.ncnn.{param,bin}.  Every block is uploaded once. */
+ * seedvr2_dit_output.ncnn.{param,bin}.  Every block is uploaded once.
+ * When model_dir holds a SHA256SUMS manifest, every file it lists is checked
+ * first (sv2_verify_checksums) and a failed check fails the load with
+ * SV2_EINVAL before any weight is read. */
 int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out);
 /* Assembles a DiT from existing heads and blocks (borrowed; they must outlive
  * the DiT and share its compute dtype). */
@@ -526,6 +547,26 @@ int sv2_euler_endpoint(const float* prediction, const float* current, float* out
                        void* stream);
 
 /* Message of the last failure on the calling thread (never NULL). */
+/* ------------------------------------------------------------------------
+ * Model integrity (scripts/verify-models.sh:17-24; download-models.sh:
+ * 93-97, :140-148).  Host only.
+ * ------------------------------------------------------------------------ */
+
+/* SHA-256 (FIPS 180-4) of `bytes` bytes at `data` into digest[32]. */
+int sv2_sha256(const void* data, size_t bytes, unsigned char digest[32]);
+
+/* SHA-256 of a whole file. */
+int sv2_sha256_file(const char* path, unsigned char digest[32]);
+
+/* `sha256sum --check --strict SHA256SUMS` in `dir`: parses the manifest
+ * (lines "<64 hex digits> <name>" or "<digest> *<name>"; blank lines skipped;
+ * names must not be empty, start with '.' or contain '/'; no extra fields)
+ * and hashes every listed file on `threads` threads (<= 0: up to 16).
+ * Returns the number of files verified, 0 when `dir` has no SHA256SUMS, or
+ * SV2_EINVAL for a malformed manifest, a listed file that is missing, or a
+ * digest that does not match (sv2_last_error names the line or file). */
+int sv2_verify_checksums(const char* dir, int threads);
+
 const char* sv2_last_error(void);
 
 /* Library version string. */

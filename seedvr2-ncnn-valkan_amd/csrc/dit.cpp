@@ -626,6 +626,10 @@ int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out)
                 return set_error(SV2_EINVAL, "sv2_dit_load: DiT model file is missing: " + path(s, ext));
             std::fclose(f);
         }
+    // the directory's SHA256SUMS, when it has one (scripts/verify-models.sh:17-24)
+    const int checked = sv2_verify_checksums(model_dir, 0);
+    if (checked < 0)
+        return checked;
     sv2_dit* d = new sv2_dit();
     d->owns = true;
     d->dtype = compute_dtype;

@@ -61,9 +61,14 @@ struct sv2_block
     size_t ws_bytes = 0;
     bool debug_on = false;
     sv2_block_debug debug{};
+    // device staging of sv2_block_forward_host, grown on demand
+    void* stage = nullptr;
+    size_t stage_bytes = 0;
 
     ~sv2_block()
     {
+        if (stage)
+            (void)hipFree(stage);
         for (void* p : owned)
             (void)hipFree(p);
         if (rope)
@@ -760,6 +765,145 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                 (Lt > 0 && (rc = capture(dbg->output_txt, txt_out, Lt, D)) != SV2_OK)))
         return rc;
     return SV2_OK;
+}
+
+int64_t sv2_block_window_rows(const sv2_block* block, int text_len)
+{
+    using namespace sv2;
+    if (!block || text_len < 0)
+        return set_error(SV2_EINVAL, "sv2_block_window_rows: bad argument");
+    if (!block->shape_valid)
+        return set_error(SV2_EINVAL, "sv2_block_window_rows: runtime shape not set");
+    const sv2_window_rule rule = block_rule(block);
+    const int n = sv2_window_plan(&rule, nullptr, 0);
+    if (n < 0)
+        return n;
+    std::vector<sv2_window> wins(n);
+    if (sv2_window_plan(&rule, wins.data(), n) != n)
+        return set_error(SV2_EINVAL, "sv2_block_window_rows: window plan changed");
+    int64_t rows = 0;
+    for (const sv2_window& w : wins)
+        rows += int64_t(w.t1 - w.t0) * (w.h1 - w.h0) * (w.w1 - w.w0) + text_len;
+    return rows;
+}
+
+int sv2_block_forward_host(sv2_block* b, const float* vid, const float* txt, int text_len, const float* emb,
+                           float* vid_out, float* txt_out, const sv2_block_debug* host_debug)
+{
+    using namespace sv2;
+    if (!b || !vid || !emb || !vid_out || text_len < 0 || (text_len > 0 && (!txt || !txt_out)))
+        return set_error(SV2_EINVAL, "sv2_block_forward_host: null argument or bad text length");
+    if (!b->shape_valid)
+        return set_error(SV2_EINVAL, "sv2_block_forward_host: set_runtime_shape was not called");
+    const int64_t D = b->cfg.dim, Lv = int64_t(b->T) * b->H * b->W, Lt = text_len;
+    const int64_t S = host_debug ? sv2_block_window_rows(b, text_len) : 0;
+    if (S < 0)
+        return static_cast<int>(S);
+    const int dt = b->dtype;
+    const size_t es = dtype_size(dt);
+
+    // staging layout: fp32 inputs and outputs, their compute-dtype copies
+    // (fp16 mode only) and the captures the caller asked for, each 256-byte aligned
+    size_t total = 0;
+    auto take = [&total](size_t bytes) {
+        const size_t at = total;
+        total += (bytes + 255) & ~size_t(255);
+        return at;
+    };
+    const size_t o_vid = take(Lv * D * 4), o_txt = take(Lt * D * 4), o_emb = take(6 * D * 4);
+    const size_t o_vout = take(Lv * D * 4), o_tout = take(Lt * D * 4);
+    const bool cast = dt != SV2_F32;
+    const size_t o_vc = cast ? take(Lv * D * es) : 0, o_tc = cast ? take(Lt * D * es) : 0;
+    const size_t o_voc = cast ? take(Lv * D * es) : 0, o_toc = cast ? take(Lt * D * es) : 0;
+    // the captures: host pointer, device offset, element count (field order of sv2_block_debug)
+    struct Capture
+    {
+        float* host;
+        size_t offset;
+        int64_t count;
+    };
+    float* sv2_block_debug::*const fields[16] = {
+        &sv2_block_debug::qkv_vid,       &sv2_block_debug::qkv_txt,       &sv2_block_debug::attention_vid,
+        &sv2_block_debug::attention_txt, &sv2_block_debug::projected_vid, &sv2_block_debug::projected_txt,
+        &sv2_block_debug::output_vid,    &sv2_block_debug::output_txt,    &sv2_block_debug::norm_q_vid,
+        &sv2_block_debug::norm_q_txt,    &sv2_block_debug::norm_k_vid,    &sv2_block_debug::norm_k_txt,
+        &sv2_block_debug::attention_q,   &sv2_block_debug::attention_k,   &sv2_block_debug::attention_v,
+        &sv2_block_debug::attention_output};
+    const int64_t counts[16] = {Lv * 3 * D, Lt * 3 * D, Lv * D, Lt * D, Lv * D, Lt * D, Lv * D, Lt * D,
+                                Lv * D,     Lt * D,     Lv * D, Lt * D, S * D,  S * D,  S * D,  S * D};
+    std::vector<Capture> caps;
+    for (int i = 0; host_debug && i < 16; i++)
+        if (host_debug->*fields[i] && counts[i] > 0)
+            caps.push_back({host_debug->*fields[i], take(size_t(counts[i]) * 4), counts[i]});
+
+    if (b->stage_bytes < total)
+    {
+        if (b->stage)
+            (void)hipFree(b->stage);
+        b->stage = nullptr;
+        b->stage_bytes = 0;
+        hipError_t err = hipMalloc(&b->stage, total);
+        if (err != hipSuccess)
+        {
+            b->stage = nullptr;
+            return hip_error(err, "sv2_block_forward_host: staging allocation");
+        }
+        b->stage_bytes = total;
+    }
+    char* st = static_cast<char*>(b->stage);
+    auto dev = [st](size_t off) { return reinterpret_cast<float*>(st + off); };
+    hipStream_t stream = nullptr;
+    hipError_t err = hipMemcpy(dev(o_vid), vid, Lv * D * 4, hipMemcpyHostToDevice);
+    if (err == hipSuccess && Lt > 0)
+        err = hipMemcpy(dev(o_txt), txt, Lt * D * 4, hipMemcpyHostToDevice);
+    if (err == hipSuccess)
+        err = hipMemcpy(dev(o_emb), emb, 6 * D * 4, hipMemcpyHostToDevice);
+    if (err != hipSuccess)
+        return hip_error(err, "sv2_block_forward_host: upload");
+    int rc = SV2_OK;
+    void* vin = dev(o_vid);
+    void* tin = dev(o_txt);
+    void* vout = dev(o_vout);
+    void* tout = dev(o_tout);
+    if (cast)
+    {
+        vin = st + o_vc;
+        tin = st + o_tc;
+        vout = st + o_voc;
+        tout = st + o_toc;
+        if ((rc = launch_from_f32(vin, dev(o_vid), dt, Lv * D, stream)) != SV2_OK ||
+            (Lt > 0 && (rc = launch_from_f32(tin, dev(o_txt), dt, Lt * D, stream)) != SV2_OK))
+            return rc;
+    }
+
+    // the captures go to the staging copies for this call only
+    const bool saved_on = b->debug_on;
+    const sv2_block_debug saved = b->debug;
+    if (host_debug)
+    {
+        sv2_block_debug d{};
+        for (const Capture& c : caps)
+            for (int i = 0; i < 16; i++)
+                if (host_debug->*fields[i] == c.host)
+                    d.*fields[i] = dev(c.offset);
+        b->debug = d;
+        b->debug_on = true;
+    }
+    rc = sv2_block_forward(b, vin, Lt > 0 ? tin : nullptr, text_len, dev(o_emb), vout, Lt > 0 ? tout : nullptr,
+                           nullptr, 0, stream);
+    b->debug_on = saved_on;
+    b->debug = saved;
+    if (rc != SV2_OK)
+        return rc;
+    if (cast && ((rc = launch_to_f32(dev(o_vout), vout, dt, Lv * D, stream)) != SV2_OK ||
+                 (Lt > 0 && (rc = launch_to_f32(dev(o_tout), tout, dt, Lt * D, stream)) != SV2_OK)))
+        return rc;
+    err = hipMemcpy(vid_out, dev(o_vout), Lv * D * 4, hipMemcpyDeviceToHost);
+    if (err == hipSuccess && Lt > 0)
+        err = hipMemcpy(txt_out, dev(o_tout), Lt * D * 4, hipMemcpyDeviceToHost);
+    for (size_t i = 0; err == hipSuccess && i < caps.size(); i++)
+        err = hipMemcpy(caps[i].host, dev(caps[i].offset), size_t(caps[i].count) * 4, hipMemcpyDeviceToHost);
+    return err == hipSuccess ? SV2_OK : hip_error(err, "sv2_block_forward_host: download");
 }
 
 int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug)

@@ -44,6 +44,11 @@ EXPORTS = [
     "sv2_block_set_runtime_shape",
     "sv2_block_workspace_size",
     "sv2_block_forward",
+    "sv2_block_window_rows",
+    "sv2_sha256",
+    "sv2_sha256_file",
+    "sv2_verify_checksums",
+    "sv2_block_forward_host",
     "sv2_block_destroy",
     "sv2_block_set_debug",
     "sv2_dit_input_load",
@@ -249,6 +254,16 @@ def load() -> ctypes.CDLL:
     lib.sv2_block_workspace_size.restype = ctypes.c_int64
     lib.sv2_block_forward.argtypes = [vp, vp, vp, i, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.sv2_block_forward.restype = i
+    lib.sv2_sha256.argtypes = [vp, ctypes.c_size_t, vp]
+    lib.sv2_sha256.restype = i
+    lib.sv2_sha256_file.argtypes = [ctypes.c_char_p, vp]
+    lib.sv2_sha256_file.restype = i
+    lib.sv2_verify_checksums.argtypes = [ctypes.c_char_p, i]
+    lib.sv2_verify_checksums.restype = i
+    lib.sv2_block_window_rows.argtypes = [vp, i]
+    lib.sv2_block_window_rows.restype = ctypes.c_int64
+    lib.sv2_block_forward_host.argtypes = [vp, vp, vp, i, vp, vp, vp, vp]
+    lib.sv2_block_forward_host.restype = i
     lib.sv2_block_set_debug.argtypes = [vp, ctypes.POINTER(BlockDebug)]
     lib.sv2_block_set_debug.restype = i
     lib.sv2_block_destroy.argtypes = [vp]
@@ -573,6 +588,10 @@ class DitBlock:
 
     def workspace_size(self, text_len) -> int:
         return check(load().sv2_block_workspace_size(self._h, text_len), "sv2_block_workspace_size")
+
+    def window_rows(self, text_len) -> int:
+        """Rows of the window-sequence order (attention_q/k/v/output captures)."""
+        return check(load().sv2_block_window_rows(self._h, text_len), "sv2_block_window_rows")
 
     def forward(self, vid, txt, emb, vid_out, txt_out, workspace=None, stream=None):
         """vid [T*H*W, dim], txt [L, dim] (compute dtype), emb [6*dim] fp32."""
@@ -970,3 +989,24 @@ def inner_product_f16(x, w, y, epilogue=EPI_STORE, w_value=None, bias=None, gate
           "sv2_inner_product_f16")
     return y
 
+
+
+def sha256(data) -> bytes:
+    """SHA-256 digest of a bytes-like object (sv2_sha256)."""
+    buf = bytes(data)
+    out = ctypes.create_string_buffer(32)
+    src = ctypes.c_char_p(buf) if buf else None
+    check(load().sv2_sha256(src, len(buf), out), "sv2_sha256")
+    return out.raw
+
+
+def sha256_file(path) -> bytes:
+    out = ctypes.create_string_buffer(32)
+    check(load().sv2_sha256_file(str(path).encode(), out), "sv2_sha256_file")
+    return out.raw
+
+
+def verify_checksums(directory, threads: int = 0) -> int:
+    """Checks `directory`/SHA256SUMS; returns the number of files verified (0
+    when there is no manifest), raises Sv2Error on a failed check."""
+    return check(load().sv2_verify_checksums(str(directory).encode(), threads), "sv2_verify_checksums")

@@ -1,0 +1,129 @@
+"""Model integrity on the host: the library's SHA-256 (FIPS 180-4) against
+Python's hashlib on the padding boundaries, streamed files and random data,
+the FIPS 180-2 appendix B examples, and the SHA256SUMS check of a model
+directory as scripts/verify-models.sh:17-24 runs it (`sha256sum --check
+--strict`, with the manifest rules of download-models.sh:93-97, :140-148),
+including sv2_dit_load refusing a directory whose manifest does not match
+before it reads any weight."""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sv2hip
+    sv2hip.load()
+    return sv2hip
+
+
+def test_fips_examples(hip):
+    # FIPS 180-2 appendix B.1 / B.2 and the empty message
+    assert hip.sha256(b"abc").hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+    assert hip.sha256(b"abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq").hex() == \
+        "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1"
+    assert hip.sha256(b"").hex() == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855"
+
+
+def test_lengths_across_padding_boundaries(hip):
+    rng = np.random.default_rng(0)
+    data = rng.integers(0, 256, 1100, dtype=np.uint8).tobytes()
+    for n in list(range(0, 200)) + [255, 256, 257, 511, 512, 513, 1000, 1023, 1024, 1100]:
+        assert hip.sha256(data[:n]) == hashlib.sha256(data[:n]).digest(), n
+
+
+def test_large_and_file(hip, tmp_path):
+    rng = np.random.default_rng(1)
+    data = rng.integers(0, 256, (9 << 20) + 37, dtype=np.uint8).tobytes()  # crosses the 4 MiB read pieces
+    assert hip.sha256(data) == hashlib.sha256(data).digest()
+    f = tmp_path / "blob.bin"
+    f.write_bytes(data)
+    assert hip.sha256_file(f) == hashlib.sha256(data).digest()
+    e = tmp_path / "empty.bin"
+    e.write_bytes(b"")
+    assert hip.sha256_file(e) == hashlib.sha256(b"").digest()
+    with pytest.raises(hip.Sv2Error):
+        hip.sha256_file(tmp_path / "missing.bin")
+
+
+def _model_dir(tmp_path, files: dict[str, bytes]):
+    for name, data in files.items():
+        (tmp_path / name).write_bytes(data)
+    return tmp_path
+
+
+def _manifest(files: dict[str, bytes], star=False, upper=False) -> str:
+    lines = []
+    for name, data in files.items():
+        d = hashlib.sha256(data).hexdigest()
+        lines.append(f"{d.upper() if upper else d} {'*' if star else ' '}{name}")
+    return "\n".join(lines) + "\n"
+
+
+FILES = {f"part_{i:02d}.bin": bytes([i]) * (1000 * i + 7) for i in range(12)}
+
+
+@pytest.mark.parametrize("threads", [1, 4, 0])
+@pytest.mark.parametrize("form", ["text", "binary", "upper"])
+def test_verify_ok(hip, tmp_path, threads, form):
+    d = _model_dir(tmp_path, FILES)
+    (d / "SHA256SUMS").write_text(_manifest(FILES, star=form == "binary", upper=form == "upper") + "\n")
+    assert hip.verify_checksums(d, threads) == len(FILES)
+
+
+def test_no_manifest_is_nothing_to_check(hip, tmp_path):
+    assert hip.verify_checksums(_model_dir(tmp_path, FILES)) == 0
+
+
+@pytest.mark.parametrize("case, expect", [
+    ("corrupt", "corrupted"),
+    ("missing", "missing"),
+    ("bad_digest", "invalid SHA256"),
+    ("extra_field", "invalid checksum line"),
+    ("slash", "unsafe file name"),
+    ("dot", "unsafe file name"),
+    ("empty", "lists no files"),
+])
+def test_verify_rejects(hip, tmp_path, case, expect):
+    files = dict(FILES)
+    d = _model_dir(tmp_path, files)
+    text = _manifest(files)
+    if case == "corrupt":
+        raw = bytearray((d / "part_05.bin").read_bytes())
+        raw[100] ^= 1
+        (d / "part_05.bin").write_bytes(bytes(raw))
+    elif case == "missing":
+        (d / "part_03.bin").unlink()
+    elif case == "bad_digest":
+        text = text.replace(hashlib.sha256(files["part_02.bin"]).hexdigest(), "z" * 64)
+    elif case == "extra_field":
+        text += hashlib.sha256(b"x").hexdigest() + "  a.bin trailing\n"
+    elif case == "slash":
+        text += hashlib.sha256(b"x").hexdigest() + "  sub/a.bin\n"
+    elif case == "dot":
+        text += hashlib.sha256(b"x").hexdigest() + "  .hidden\n"
+    elif case == "empty":
+        text = "\n\n"
+    (d / "SHA256SUMS").write_text(text)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.verify_checksums(d)
+    assert expect in str(err.value), str(err.value)
+    if case == "corrupt":
+        assert "part_05.bin" in str(err.value)
+
+
+def test_dit_load_refuses_a_bad_manifest(hip, tmp_path):
+    """All 34 model files present, one listed with a wrong digest: the load
+    fails on the checksum before any weight is read or uploaded."""
+    names = ["seedvr2_dit_input", "seedvr2_dit_output"] + [f"seedvr2_dit_block_{i:02d}" for i in range(32)]
+    files = {f"{n}.ncnn{ext}": f"{n}{ext}".encode() for n in names for ext in (".param", ".bin")}
+    d = _model_dir(tmp_path, files)
+    text = _manifest(files)
+    (d / "seedvr2_dit_block_17.ncnn.bin").write_bytes(b"tampered")
+    (d / "SHA256SUMS").write_text(text)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.Dit.load(d, hip.F16)
+    assert "seedvr2_dit_block_17.ncnn.bin is corrupted" in str(err.value), str(err.value)
