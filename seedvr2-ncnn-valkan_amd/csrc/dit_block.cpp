@@ -1,8 +1,10 @@
 // The SeedVR2DiTBlock layer on the device (src/layers/seedvr2_dit_block.{h,cpp}
 // of the reference): parameters, weight loading from the exported
 // .param/.bin pair, and the block forward as a chain of the library's kernels
-// on one stream — token RMSNorm + ada, the QKV / proj / MLP InnerProducts as
-// rocBLAS GEMMs, the windowed attention, gated residuals and SwiGLU.
+// on one stream — token RMSNorm + ada, the QKV / proj / MLP InnerProducts
+// (hipBLASLt in fp16, the fp64-accumulating exact GEMM in the fp32 parity
+// mode, or the fused MFMA kernel under param 14), the windowed attention,
+// gated residuals and SwiGLU.
 #include <algorithm>
 #include <cstring>
 #include <string>
