@@ -9,9 +9,15 @@
 // the CPU restatement evaluates it, W [out][in] row-major, y = W x + b.
 //
 // On the VALU in fp64 (an fp64 MFMA would sum four products per step in its
-// own order).  One 256-thread workgroup per 64 x 128 tile of y; each thread
-// keeps an 8 x 4 block of double accumulators; k moves through LDS in stages
-// of 8, held as double, two stages in flight.
+// own order).  Two forms of the same arithmetic:
+//   * tiled (rows > 16): one 256-thread workgroup per 64 x 128 tile of y;
+//     each thread keeps an 8 x 4 block of double accumulators; k moves
+//     through LDS in stages of 8, held as double, two stages in flight;
+//   * few rows (rows <= 16, e.g. the DiT's one-row time MLP): one 256-thread
+//     workgroup per 64 output columns, so a wide product still spreads over
+//     many CUs; thread (c, s) owns column c for rows s, s + 4, s + 8, s + 12;
+//     W moves through LDS in chunks of 64 k, transposed so that the 64
+//     columns a wave reads at one k are consecutive.
 #include "sv2_internal.h"
 
 namespace sv2
@@ -123,6 +129,70 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(const float* __rest
     }
 }
 
+constexpr int kRowsSmall = 16; // the few-rows form handles up to this many rows
+constexpr int kCols = 64;      // output columns per few-rows workgroup
+constexpr int kChunk = 64;     // k per LDS chunk of the few-rows form
+
+__global__ __launch_bounds__(256) void gemv_f32_exact_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             const float* __restrict__ bias, float* __restrict__ y,
+                                                             int rows, int in, int out)
+{
+    __shared__ float wt[kChunk][kCols];     // wt[k][c] = W[col0 + c][k0 + k]
+    __shared__ float xs[kRowsSmall][kChunk]; // xs[r][k] = x[r][k0 + k]
+    const int tid = threadIdx.x;
+    const int c = tid & (kCols - 1);
+    const int slot = tid >> 6; // rows slot, slot + 4, slot + 8, slot + 12
+    const int col0 = blockIdx.x * kCols;
+    // W staging: thread t loads 16 consecutive k of row t / 4 of the tile
+    const int wr = tid >> 2;
+    const int wk = (tid & 3) * 16;
+    const bool w_ok = col0 + wr < out;
+    const float* wp = w + static_cast<long long>(w_ok ? col0 + wr : 0) * in;
+
+    double acc[kRowsSmall / 4];
+#pragma unroll
+    for (int i = 0; i < kRowsSmall / 4; i++)
+        acc[i] = 0.0;
+
+    for (int k0 = 0; k0 < in; k0 += kChunk)
+    {
+        // values past the edges are zero: their products are +0 and the
+        // running sums, which start at +0, stay what they were
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+        {
+            const int k = k0 + wk + e;
+            wt[wk + e][wr] = (w_ok && k < in) ? wp[k] : 0.f;
+        }
+        for (int i = tid; i < kRowsSmall * kChunk; i += 256)
+        {
+            const int r = i / kChunk;
+            const int k = k0 + i % kChunk;
+            xs[r][i % kChunk] = (r < rows && k < in) ? x[static_cast<long long>(r) * in + k] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < kChunk; k++)
+        {
+            const double wv = static_cast<double>(wt[k][c]);
+#pragma unroll
+            for (int i = 0; i < kRowsSmall / 4; i++)
+                acc[i] = __builtin_fma(static_cast<double>(xs[slot + 4 * i][k]), wv, acc[i]);
+        }
+        __syncthreads();
+    }
+    if (col0 + c >= out)
+        return;
+    const double bv = bias ? static_cast<double>(bias[col0 + c]) : 0.0;
+#pragma unroll
+    for (int i = 0; i < kRowsSmall / 4; i++)
+    {
+        const int r = slot + 4 * i;
+        if (r < rows)
+            y[static_cast<long long>(r) * out + col0 + c] = static_cast<float>(acc[i] + bv);
+    }
+}
+
 } // namespace
 
 int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x, const float* w, const float* bias,
@@ -134,6 +204,13 @@ int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x
         return SV2_OK;
     if (!x || !w || !y)
         return set_error(SV2_EINVAL, "inner product (fp32): null pointer");
+    if (rows <= kRowsSmall)
+    {
+        hipLaunchKernelGGL(gemv_f32_exact_kernel, dim3(static_cast<unsigned>((out + kCols - 1) / kCols)), dim3(256), 0,
+                           stream, x, w, bias, y, rows, in, out);
+        const hipError_t err = hipGetLastError();
+        return err == hipSuccess ? SV2_OK : hip_error(err, "gemv_f32_exact_kernel launch");
+    }
     const dim3 grid(static_cast<unsigned>((out + kBN - 1) / kBN), static_cast<unsigned>((rows + kBM - 1) / kBM));
     if (grid.y > 65535u)
         return set_error(SV2_EUNSUPPORTED, "inner product (fp32): too many rows");

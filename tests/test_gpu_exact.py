@@ -34,6 +34,10 @@ def differing(a, b) -> int:
 
 @pytest.mark.parametrize("rows,k,n,bias", [
     (1, 256, 2560, True),        # the time MLP's first product (one row)
+    (1, 2560, 15360, True),      # the time MLP's last product (six modulation slots)
+    (3, 2560, 2560, False),      # a few rows
+    (16, 100, 130, True),        # the most rows of the few-rows form, k and n ragged
+    (17, 64, 128, True),         # the fewest rows of the tiled form
     (65, 132, 2560, True),       # vid_in: 4 x 33 latent channels, a ragged row tile
     (130, 2560, 64, True),       # the output head's projection (4 x 16 outputs)
     (300, 2560, 7680, False),    # qkv
