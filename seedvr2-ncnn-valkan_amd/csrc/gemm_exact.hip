@@ -13,11 +13,10 @@
 //   * tiled (rows > 16): one 256-thread workgroup per 64 x 128 tile of y;
 //     each thread keeps an 8 x 4 block of double accumulators; k moves
 //     through LDS in stages of 8, held as double, two stages in flight;
-//   * few rows (rows <= 16, e.g. the DiT's one-row time MLP): one 256-thread
-//     workgroup per 64 output columns, so a wide product still spreads over
-//     many CUs; thread (c, s) owns column c for rows s, s + 4, s + 8, s + 12;
-//     W moves through LDS in chunks of 64 k, transposed so that the 64
-//     columns a wave reads at one k are consecutive.
+//   * few rows (rows <= 16, e.g. the DiT's one-row time MLP): one one-wave
+//     workgroup per 16 output columns, so a wide product spreads over many
+//     CUs and several workgroups share each; W moves through LDS in chunks of
+//     64 k, transposed, the next chunk loaded into registers meanwhile.
 #include "sv2_internal.h"
 
 namespace sv2
@@ -130,54 +129,71 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(const float* __rest
 }
 
 constexpr int kRowsSmall = 16; // the few-rows form handles up to this many rows
-constexpr int kCols = 64;      // output columns per few-rows workgroup
+constexpr int kCols = 16;      // output columns per few-rows workgroup (one wave)
 constexpr int kChunk = 64;     // k per LDS chunk of the few-rows form
 
-__global__ __launch_bounds__(256) void gemv_f32_exact_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                             const float* __restrict__ bias, float* __restrict__ y,
-                                                             int rows, int in, int out)
+// One wave: lane (c, s) = (lane % 16, lane / 16) owns column col0 + c for
+// rows s, s + 4, s + 8, s + 12.  Lane l stages 16 consecutive k of W row
+// col0 + l / 4, and loads the next chunk's into registers while the current
+// chunk is summed; several of these small workgroups share a CU and hide
+// each other's loads.
+__global__ __launch_bounds__(64) void gemv_f32_exact_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            const float* __restrict__ bias, float* __restrict__ y,
+                                                            int rows, int in, int out)
 {
-    __shared__ float wt[kChunk][kCols];     // wt[k][c] = W[col0 + c][k0 + k]
+    __shared__ float wt[kChunk][kCols];      // wt[k][c] = W[col0 + c][k0 + k]
     __shared__ float xs[kRowsSmall][kChunk]; // xs[r][k] = x[r][k0 + k]
-    const int tid = threadIdx.x;
-    const int c = tid & (kCols - 1);
-    const int slot = tid >> 6; // rows slot, slot + 4, slot + 8, slot + 12
+    const int lane = threadIdx.x;
+    const int c = lane & (kCols - 1);
+    const int slot = lane >> 4;
     const int col0 = blockIdx.x * kCols;
-    // W staging: thread t loads 16 consecutive k of row t / 4 of the tile
-    const int wr = tid >> 2;
-    const int wk = (tid & 3) * 16;
+    const int wr = lane >> 2;
+    const int wk = (lane & 3) * 16;
     const bool w_ok = col0 + wr < out;
     const float* wp = w + static_cast<long long>(w_ok ? col0 + wr : 0) * in;
+
+    // values past the edges are zero: their products are +0 and the running
+    // sums, which start at +0, stay what they were
+    float wv[16];
+    auto load_w = [&](int k0) {
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+        {
+            const int k = k0 + wk + e;
+            wv[e] = (w_ok && k < in) ? wp[k] : 0.f;
+        }
+    };
 
     double acc[kRowsSmall / 4];
 #pragma unroll
     for (int i = 0; i < kRowsSmall / 4; i++)
         acc[i] = 0.0;
 
+    load_w(0);
     for (int k0 = 0; k0 < in; k0 += kChunk)
     {
-        // values past the edges are zero: their products are +0 and the
-        // running sums, which start at +0, stay what they were
 #pragma unroll
         for (int e = 0; e < 16; e++)
+            wt[wk + e][wr] = wv[e];
+#pragma unroll
+        for (int j = 0; j < kRowsSmall * kChunk / 64; j++)
         {
-            const int k = k0 + wk + e;
-            wt[wk + e][wr] = (w_ok && k < in) ? wp[k] : 0.f;
-        }
-        for (int i = tid; i < kRowsSmall * kChunk; i += 256)
-        {
+            const int i = lane + 64 * j;
             const int r = i / kChunk;
             const int k = k0 + i % kChunk;
             xs[r][i % kChunk] = (r < rows && k < in) ? x[static_cast<long long>(r) * in + k] : 0.f;
         }
         __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < kChunk; k++)
-        {
-            const double wv = static_cast<double>(wt[k][c]);
+        if (k0 + kChunk < in)
+            load_w(k0 + kChunk);
 #pragma unroll
-            for (int i = 0; i < kRowsSmall / 4; i++)
-                acc[i] = __builtin_fma(static_cast<double>(xs[slot + 4 * i][k]), wv, acc[i]);
+        for (int i = 0; i < kRowsSmall / 4; i++)
+        {
+            if (slot + 4 * i >= rows) // rows past the input: nothing to sum
+                break;
+#pragma unroll 16
+            for (int k = 0; k < kChunk; k++)
+                acc[i] = __builtin_fma(static_cast<double>(xs[slot + 4 * i][k]), static_cast<double>(wt[k][c]), acc[i]);
         }
         __syncthreads();
     }
@@ -206,7 +222,7 @@ int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x
         return set_error(SV2_EINVAL, "inner product (fp32): null pointer");
     if (rows <= kRowsSmall)
     {
-        hipLaunchKernelGGL(gemv_f32_exact_kernel, dim3(static_cast<unsigned>((out + kCols - 1) / kCols)), dim3(256), 0,
+        hipLaunchKernelGGL(gemv_f32_exact_kernel, dim3(static_cast<unsigned>((out + kCols - 1) / kCols)), dim3(64), 0,
                            stream, x, w, bias, y, rows, in, out);
         const hipError_t err = hipGetLastError();
         return err == hipSuccess ? SV2_OK : hip_error(err, "gemv_f32_exact_kernel launch");
