@@ -261,7 +261,9 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
     const size_t es = dtype_size(b->dtype);
     const size_t D = b->cfg.dim, F = b->cfg.mlp_hidden;
     const size_t Lv = static_cast<size_t>(b->T) * b->H * b->W, Lt = text_len;
-    const size_t R = std::max(Lv, Lt);
+    // rows of the normalised input and of the MLP's gate / value: the video
+    // and text rows together when the row-wise steps run merged
+    const size_t R = Lv + Lt;
     sv2_attn_args a = attention_args(b, text_len);
     a.vid_qkv = reinterpret_cast<const void*>(16); // placeholders: the size query reads no memory
     a.txt_qkv = reinterpret_cast<const void*>(16);
@@ -621,19 +623,34 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     if ((rc = launch_ada_table(emb, vb.ada[1], vb.ada[2], 0, D, tab_va, stream)) != SV2_OK ||
         (rc = launch_ada_table(emb, vb.ada[4], vb.ada[5], 3, D, tab_vm, stream)) != SV2_OK)
         return rc;
-    if (Lt > 0 && ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
-                   (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
+    const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
+    // With shared weights outside the last layer the text rows get the video
+    // rows' treatment in every step but the attention: the same branch (:1139)
+    // and the same ada slots of the same emb, so the same tables.  When the
+    // caller's text rows follow its video rows in memory (as the DiT lays its
+    // hidden streams out) and this layout's text regions follow the video
+    // ones, each row-wise step (RMSNorm + ada, the InnerProducts, the gated
+    // residuals, SwiGLU) runs once over all Lv + Lt rows.
+    const size_t row_bytes = static_cast<size_t>(D) * es;
+    const bool merged = c.shared_weights && !c.last_layer && Lt > 0 && !dbg &&
+                        static_cast<const char*>(txt) == static_cast<const char*>(vid) + Lv * row_bytes &&
+                        static_cast<const char*>(txt_out) == static_cast<const char*>(vid_out) + Lv * row_bytes &&
+                        qkv_t == qkv_v + 3 * Lv * row_bytes && att_t == att_v + Lv * row_bytes &&
+                        p_t == p_v + Lv * row_bytes;
+    const int Lr = merged ? Lv + Lt : Lv; // rows of the video branch's row-wise steps
+    if (Lt > 0 && !merged &&
+        ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
+         (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
         return rc;
     // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
-    if ((rc = launch_rmsnorm_table(vid, xa, dt, Lv, D, c.norm_eps, tab_va, vb.ada[0], nullptr, 1, stream)) != SV2_OK)
+    if ((rc = launch_rmsnorm_table(vid, xa, dt, Lr, D, c.norm_eps, tab_va, vb.ada[0], nullptr, 1, stream)) != SV2_OK)
         return rc;
-    const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
-    // the video branch on the fused MFMA InnerProducts (param 14); the text
-    // rows (a few dozen) stay on the library GEMMs
+    // the video branch on the fused MFMA InnerProducts (param 14); unmerged
+    // text rows (a few dozen) stay on the library GEMMs
     const bool fused = c.fused_gemm && dt == SV2_F16 && !dbg;
-    if ((rc = fused ? gemm_mfma(stream, Lv, D, 3 * D, xa, vb.w_qkv, nullptr, qkv_v, kGemmStore, nullptr, nullptr,
+    if ((rc = fused ? gemm_mfma(stream, Lr, D, 3 * D, xa, vb.w_qkv, nullptr, qkv_v, kGemmStore, nullptr, nullptr,
                                 nullptr)
-                    : gemm_rows(stream, dt, Lv, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
+                    : gemm_rows(stream, dt, Lr, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
         return rc;
     auto capture = [&](float* dst, const void* src, int rows, int cols) {
         return dst ? launch_to_f32(dst, src, dt, static_cast<long long>(rows) * cols, stream) : SV2_OK;
@@ -654,7 +671,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     const float* tbias_in_residual = dt == SV2_F32 ? nullptr : tb.b_proj;
     if (dbg && (rc = capture(dbg->qkv_vid, qkv_v, Lv, 3 * D)) != SV2_OK)
         return rc;
-    if (Lt > 0)
+    if (Lt > 0 && !merged)
     {
         if ((rc = launch_rmsnorm_table(txt, xa, dt, Lt, D, c.norm_eps, tab_ta, tb.ada[0], nullptr,
                                        c.last_layer ? 0 : 1, stream)) != SV2_OK)
@@ -701,7 +718,7 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
     // output projections; their bias is added in the gated residual (:1180-1209)
     if (fused)
     {
-        if ((rc = gemm_mfma(stream, Lv, D, D, att_v, vb.w_proj, nullptr, p_v, kGemmResidual, vb.b_proj,
+        if ((rc = gemm_mfma(stream, Lr, D, D, att_v, vb.w_proj, nullptr, p_v, kGemmResidual, vb.b_proj,
                             tab_va + 2 * D, vid)) != SV2_OK)
             return rc;
     }
@@ -719,21 +736,21 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
                 if ((rc = launch_gated_bias(tab_va + 2 * D, vb.b_proj, gated_bias, D, stream)) != SV2_OK)
                     return rc;
             }
-            rc = gemm_rows_gated(stream, dt, Lv, D, D, att_v, vb.w_proj, p_v, tab_va + 2 * D, vid, gated_bias);
+            rc = gemm_rows_gated(stream, dt, Lr, D, D, att_v, vb.w_proj, p_v, tab_va + 2 * D, vid, gated_bias);
             if (rc != SV2_OK && rc != SV2_EUNSUPPORTED)
                 return rc;
         }
         if (rc == SV2_EUNSUPPORTED)
         {
-            if ((rc = gemm_rows_bias(stream, dt, Lv, D, D, att_v, vb.w_proj, vbias_in_product, p_v)) != SV2_OK)
+            if ((rc = gemm_rows_bias(stream, dt, Lr, D, D, att_v, vb.w_proj, vbias_in_product, p_v)) != SV2_OK)
                 return rc;
             if (dbg && (rc = capture_projected(dbg->projected_vid, p_v, vbias_in_residual, Lv)) != SV2_OK)
                 return rc;
-            if ((rc = launch_residual_table(p_v, vid, dt, Lv, D, tab_va, vbias_in_residual, 0, stream)) != SV2_OK)
+            if ((rc = launch_residual_table(p_v, vid, dt, Lr, D, tab_va, vbias_in_residual, 0, stream)) != SV2_OK)
                 return rc;
         }
     }
-    if (Lt > 0)
+    if (Lt > 0 && !merged)
     {
         if ((rc = gemm_rows_bias(stream, dt, Lt, D, D, att_t, tb.w_proj, tbias_in_product, p_t)) != SV2_OK)
             return rc;
@@ -745,9 +762,9 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
             return rc;
     }
     // MLPs (:1211-1260); the last layer's text output is 2 * txt_proj (:1225-1246)
-    if ((rc = branch_mlp(b, stream, vb, tab_vm, p_v, Lv, vid_out, xa, g, u, fused)) != SV2_OK)
+    if ((rc = branch_mlp(b, stream, vb, tab_vm, p_v, Lr, vid_out, xa, g, u, fused)) != SV2_OK)
         return rc;
-    if (Lt > 0)
+    if (Lt > 0 && !merged)
     {
         if (c.last_layer)
         {

@@ -486,3 +486,52 @@ def test_debug_captures_match_the_oracle(hip, orc, device, variant, dtype):
         rep = report(g["attention_output"], out_ref)
         print(f"  attention_output: {rep}", flush=True)
         assert_parity(rep, "attention_output")
+
+
+# ---- shared-weight blocks with the text rows after the video rows ----------
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("grid,L,shifted", [((3, 8, 12), 7, False), ((2, 16, 30), 58, True)],
+                         ids=["small", "480x256x5-dims"])
+def test_shared_block_rows_merged(hip, orc, device, dtype, grid, L, shifted):
+    """A shared-weight block (blocks >= 10 of the exporter's layout, not the
+    last) whose text rows follow its video rows in one buffer, as the DiT lays
+    out its hidden streams: every row-wise step then runs once over all rows.
+    Against the same block on separate video and text buffers: bit for bit in
+    fp32 (every kernel of the row-wise steps computes a row the same way
+    whatever the row count), and within the block gate in fp16 (a product of
+    more rows may run on another library kernel); both against the oracle."""
+    T, H, W = grid
+    dim, heads, hidden = 256, 2, 512
+    code = hip.F32 if dtype == "f32" else hip.F16
+    td = torch.float32 if dtype == "f32" else torch.float16
+    print(f"[merged rows] grid={grid} L={L} {dtype}", flush=True)
+    cfg = hip.block_config(dim=dim, heads=heads, mlp_hidden=hidden, shared_weights=1, shifted_window=int(shifted))
+    rng = np.random.default_rng(31)
+    w = nf.random_weights(rng, dim, hidden, shared=True)
+    Lv = T * H * W
+    vid = rng.standard_normal((Lv, dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    txt = rng.standard_normal((L, dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    emb = rng.standard_normal(6 * dim, dtype=np.float32)
+    blk = hip.DitBlock.from_host(cfg, w, code)
+    try:
+        blk.set_runtime_shape(T, H, W)
+        e = torch.from_numpy(emb).to(device)
+        rows_in = torch.from_numpy(np.concatenate([vid, txt])).to(device=device, dtype=td)
+        rows_out = torch.full_like(rows_in, float("nan"))
+        blk.forward(rows_in[:Lv], rows_in[Lv:], e, rows_out[:Lv], rows_out[Lv:])
+        sep_v, sep_t = run_gpu(hip, blk, vid, txt, emb, T, H, W, device)
+        torch.cuda.synchronize()
+        mv, mt = (t.float().cpu().numpy() for t in (rows_out[:Lv], rows_out[Lv:]))
+    finally:
+        blk.close()
+    if dtype == "f32":
+        assert np.array_equal(mv.view(np.uint32), sep_v.view(np.uint32))
+        assert np.array_equal(mt.view(np.uint32), sep_t.view(np.uint32))
+    else:
+        for a, b in ((mv, sep_v), (mt, sep_t)):
+            rep = metrics(a, b)
+            assert rep["finite"] and rep["nrmse"] <= TOL_NRMSE and rep["cosine"] >= 0.99999, rep
+    rv, rt = oracle_block(orc, w, vid, txt, emb, T, H, W, cfg)
+    assert_block(metrics(mv, rv), code, hip, "merged vid")
+    assert_block(metrics(mt, rt), code, hip, "merged txt")
