@@ -287,8 +287,10 @@ int64_t sv2_block_workspace_size(const sv2_block* block, int text_len);
  * 1114-1267): vid [T*H*W, dim] and txt [text_len, dim] in the compute dtype,
  * emb [6*dim] fp32; writes vid_out, txt_out (same shapes, compute dtype).
  * Enqueues on `stream` only.  workspace may be NULL (the block then keeps
- * its own, grown on demand).  Returns SV2_EINVAL when the runtime shape was
- * not set (as the layer's device forward, :1320-1321). */
+ * its own, grown on demand; forwards of one block that may run at the same
+ * time, on different streams, must then each pass their own workspace).
+ * Returns SV2_EINVAL when the runtime shape was not set (as the layer's
+ * device forward, :1320-1321). */
 int sv2_block_forward(sv2_block* block, const void* vid, const void* txt, int text_len, const float* emb,
                       void* vid_out, void* txt_out, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -308,7 +310,9 @@ int64_t sv2_block_window_rows(const sv2_block* block, int text_len);
  * for this call (the sizes of sv2_block_debug).  Stages everything through
  * device memory the block keeps (grown on demand), runs on the null stream
  * and returns when the outputs are on the host.  This is the entry point of
- * the ncnn layer adapter; device callers use sv2_block_forward. */
+ * the ncnn layer adapter; device callers use sv2_block_forward.  The staging
+ * memory and the workspace belong to the block: calls on one block must not
+ * overlap (different blocks are independent). */
 int sv2_block_forward_host(sv2_block* block, const float* vid, const float* txt, int text_len, const float* emb,
                            float* vid_out, float* txt_out, const struct sv2_block_debug* host_debug);
 
