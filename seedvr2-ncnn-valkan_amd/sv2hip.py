@@ -602,6 +602,35 @@ class DitBlock:
                                        _ptr(txt_out), _ptr(workspace), ws_bytes, _stream(stream)),
               "sv2_block_forward")
 
+    def forward_host(self, vid, txt, emb, captures: dict | None = None):
+        """The host-buffer forward (sv2_block_forward_host): vid [T*H*W, dim],
+        txt [L, dim], emb [6*dim] fp32 host arrays; returns (vid_out, txt_out)
+        as fp32 numpy arrays.  captures: {field: fp32 host array} of
+        BLOCK_DEBUG_FIELDS to fill during this call."""
+        dim = self.config.dim
+        vid = np.ascontiguousarray(vid, dtype=np.float32)
+        txt = np.ascontiguousarray(np.zeros((0, dim), np.float32) if txt is None else txt, dtype=np.float32)
+        emb = np.ascontiguousarray(emb, dtype=np.float32).reshape(-1)
+        if vid.ndim != 2 or vid.shape[1] != dim or txt.ndim != 2 or txt.shape[1] != dim or emb.size != 6 * dim:
+            raise ValueError("forward_host: vid/txt must be [rows, dim] and emb [6*dim]")
+        vo = np.empty_like(vid)
+        to = np.empty_like(txt)
+        dbg = None
+        if captures:
+            dbg = BlockDebug()
+            for k, a in captures.items():
+                if k not in BLOCK_DEBUG_FIELDS:
+                    raise KeyError(k)
+                if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags.c_contiguous):
+                    raise ValueError(f"{k}: host captures are contiguous fp32 numpy arrays")
+                setattr(dbg, k, a.ctypes.data)
+        L = txt.shape[0]
+        check(load().sv2_block_forward_host(self._h, vid.ctypes.data, txt.ctypes.data if L else None, L,
+                                            emb.ctypes.data, vo.ctypes.data, to.ctypes.data if L else None,
+                                            ctypes.byref(dbg) if dbg is not None else None),
+              "sv2_block_forward_host")
+        return vo, to
+
     def set_debug(self, captures: dict | None):
         """captures: {field: fp32 contiguous device tensor} for fields of
         BLOCK_DEBUG_FIELDS, or None to stop capturing."""
