@@ -535,3 +535,33 @@ def test_shared_block_rows_merged(hip, orc, device, dtype, grid, L, shifted):
     rv, rt = oracle_block(orc, w, vid, txt, emb, T, H, W, cfg)
     assert_block(metrics(mv, rv), code, hip, "merged vid")
     assert_block(metrics(mt, rt), code, hip, "merged txt")
+
+
+def test_forward_host_equals_device_forward(hip, device):
+    """sv2_block_forward_host (the ncnn layer's CPU-signature forward, host
+    fp32 blobs staged through device memory) against sv2_block_forward on
+    device buffers: the same kernels, bit for bit in the fp32 mode, with a
+    host capture filled in the same call; a second call with fewer text
+    tokens reuses the block's staging."""
+    dim, heads, hidden = 256, 2, 512
+    rng = np.random.default_rng(77)
+    w = nf.random_weights(rng, dim, hidden, shared=False)
+    cfg = hip.block_config(dim=dim, heads=heads, mlp_hidden=hidden, shifted_window=1)
+    blk = hip.DitBlock.from_host(cfg, w, hip.F32)
+    try:
+        blk.set_runtime_shape(3, 8, 12)
+        for L in (7, 3):
+            vid = rng.standard_normal((288, dim), dtype=np.float32)
+            txt = rng.standard_normal((L, dim), dtype=np.float32)
+            emb = rng.standard_normal(6 * dim, dtype=np.float32)
+            cap = np.full((288, 3 * dim), np.nan, np.float32)
+            hv, ht = blk.forward_host(vid, txt, emb, captures={"qkv_vid": cap})
+            dcap = torch.full((288, 3 * dim), float("nan"), device=device)
+            blk.set_debug({"qkv_vid": dcap})
+            dv, dt = run_gpu(hip, blk, vid, txt, emb, 3, 8, 12, device)
+            blk.set_debug(None)
+            assert np.array_equal(hv.view(np.uint32), dv.view(np.uint32))
+            assert np.array_equal(ht.view(np.uint32), dt.view(np.uint32))
+            assert np.array_equal(cap.view(np.uint32), dcap.cpu().numpy().view(np.uint32))
+    finally:
+        blk.close()
