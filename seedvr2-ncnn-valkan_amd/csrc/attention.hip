@@ -64,6 +64,7 @@ constexpr int kBlockN = 64;                  // keys per tile
 constexpr int kTileBytes = kBlockN * kHeadDim * 2; // one K, V or V^T tile of 16-bit values
 constexpr int kVtStride = 64;                // halfs per row of the transposed value tile (swizzled)
 constexpr int kTextPad = 64;                 // text rows of the prepared workspace are padded to this
+constexpr int kDirectTextTiles = 2;          // text tiles fetched before the loop come as finished V^T tiles
 constexpr int kMaxVideoRows = 4096;          // video tokens per window (local coordinates fit 10 bits)
 constexpr int kPrepRows = 16;                // text rows per text_prepare workgroup
 constexpr int kMaxLds = 160 * 1024;          // LDS of one gfx950 CU
@@ -293,6 +294,8 @@ struct AttnParams
     uint16_t* txt_q;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_k;        // [heads][text_len][128] bf16, prepared
     uint16_t* txt_vt;       // [heads][text_pad][128] P*V operand type, prepared
+    uint16_t* txt_vlds;     // [heads][kDirectTextTiles][64 * 128]: the first text tiles' V^T
+                            // in the byte order of an LDS V^T tile (16-bit inputs)
     float* nq_txt;          // optional debug captures [text_len][D]: text q, k after the norm, before RoPE
     float* nk_txt;
     int ordered;            // windows dispatched in the order of `order` (else in plan order)
@@ -951,8 +954,25 @@ __global__ __launch_bounds__(256) void text_prepare_kernel(AttnParams p)
     }
     // rows past text_len are zero (+0.0 is the all-zero pattern in fp16 and
     // bf16 alike): masked keys then multiply finite values
-    *reinterpret_cast<uint4*>(p.txt_vt + (static_cast<long long>(head) * p.text_pad + l) * kHeadDim + d0) =
-        valid ? v_operand8<TI>(v) : make_uint4(0u, 0u, 0u, 0u);
+    const uint4 vop = valid ? v_operand8<TI>(v) : make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(p.txt_vt + (static_cast<long long>(head) * p.text_pad + l) * kHeadDim + d0) = vop;
+    if constexpr (TI::kDma)
+    {
+        // the first text tiles also as V^T tiles in LDS byte order: dim d of
+        // key j sits at element vt_offset(d, j / 8) + j % 8 of its tile, the
+        // layout the value waves' transpose writes, so the attention kernel
+        // copies these tiles into LDS unchanged
+        if (l < kDirectTextTiles * kBlockN)
+        {
+            uint16_t* tile = p.txt_vlds + (static_cast<long long>(head) * kDirectTextTiles + l / kBlockN) *
+                                              (kBlockN * kHeadDim);
+            const int j = l % kBlockN;
+            const uint32_t w[4] = {vop.x, vop.y, vop.z, vop.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                tile[vt_offset(d0 + e, j >> 3) + (j & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        }
+    }
 }
 
 // ---------------------------------------------------------------- key/value tiles
@@ -1013,10 +1033,22 @@ __device__ inline void dma_tile(const AttnParams& p, const Geometry& gm, const S
             dma16(krow + 8 * (8 * i + ksl), kt + i * 8192 + 8 * wave * 128);
         return;
     }
+    const int v = wave - 8;
+    if (kb < gm.ntb && kb < kDirectTextTiles)
+    {
+        // the first text tiles come as finished V^T tiles: a straight copy
+        // into the V^T slot (free: these tiles are fetched before the loop)
+        const uint16_t* src = p.txt_vlds + (static_cast<long long>(head) * kDirectTextTiles + kb) *
+                                               (kBlockN * kHeadDim);
+        char* dst = vt_tile(smem, p, kb);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            dma16(src + (q * 4096 + 1024 * v) / 2 + 8 * lane, dst + q * 4096 + 1024 * v);
+        return;
+    }
     // value rows: instruction q writes LDS bytes q * 4096 + 1024 v + 16 lane,
     // i.e. chunk 4q + (lane & 3) of row 16v + lane / 4 (vq_offset)
     char* vt = vraw_tile(smem, p, kb);
-    const int v = wave - 8;
     const int r = 16 * v + (lane >> 2);
     const uint16_t* vrow;
     if (kb < gm.ntb)
@@ -1095,6 +1127,8 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
         }
         return;
     }
+    if (kb < gm.ntb && kb < kDirectTextTiles)
+        return; // copied in finished (dma_tile)
     const char* vr = vraw_tile(smem, p, kb);
     char* vt = vt_tile(smem, p, kb);
     const int q = lane >> 4;
@@ -1931,6 +1965,7 @@ struct Workspace
     int64_t txt_q;
     int64_t txt_k;
     int64_t txt_vt;
+    int64_t txt_vlds;
     int64_t seq_q; // exact mode: q, k, v after the prologue, window-sequence order, fp32
     int64_t seq_k;
     int64_t seq_v;
@@ -1954,6 +1989,8 @@ Workspace workspace_layout(const AttnParams& p)
     off = align256(off + static_cast<int64_t>(p.heads) * p.text_len * kHeadDim * 2);
     w.txt_vt = off;
     off = align256(off + static_cast<int64_t>(p.heads) * kHeadDim * p.text_pad * 2);
+    w.txt_vlds = off;
+    off = align256(off + static_cast<int64_t>(p.heads) * kDirectTextTiles * kBlockN * kHeadDim * 2);
     if (p.text_len == 0)
         off = 0;
     w.seq_q = w.seq_k = w.seq_v = off;
@@ -2123,6 +2160,7 @@ int bind_workspace(const sv2_attn_args* a, AttnParams* p)
     p->txt_q = reinterpret_cast<uint16_t*>(base + w.txt_q);
     p->txt_k = reinterpret_cast<uint16_t*>(base + w.txt_k);
     p->txt_vt = reinterpret_cast<uint16_t*>(base + w.txt_vt);
+    p->txt_vlds = reinterpret_cast<uint16_t*>(base + w.txt_vlds);
     return SV2_OK;
 }
 
