@@ -5,13 +5,15 @@
 //
 //   Y[m][n] = epilogue(sum_k X[m][k] * W[n][k])      X [M][K], W [N][K] fp16
 //
-// One 512-thread workgroup computes a 256 x 256 tile of Y, two waves per
-// SIMD (one hides the other's barrier and LDS waits), each wave a 128 x 64
-// block as 4 x 2 MFMA tiles of 32 x 32 (v_mfma_f32_32x32x16_f16, fp32
-// accumulators).  K advances in stages of 64 (whole 128-byte lines of every
-// row) through two LDS stages (32 KB of W rows + 32 KB of X rows each),
-// the next filled by global_load_lds while the current one is multiplied:
-// one barrier per stage and no staging registers.
+// One 256-thread workgroup computes a 256 x 256 tile of Y, one wave per
+// SIMD, each wave a 128 x 128 block as 4 x 4 MFMA tiles of 32 x 32
+// (v_mfma_f32_32x32x16_f16, 256 fp32 accumulators per lane).  K advances in
+// stages of 64 (whole 128-byte lines of every row: half-line stages halve the
+// fetch rate) through two 64 KB LDS slots.  A stage goes global -> registers
+// -> LDS: buffer loads two iterations ahead into one of two register sets,
+// then ds_write_b128 in four parts spread over the iteration before it is
+// multiplied, so the LDS writes share the bandwidth evenly with the operand
+// reads.  One barrier per stage, three quarters through it.
 // The products are computed transposed (W as the A operand), so a lane holds
 // four consecutive columns of one output row; the tile is rounded to fp16
 // (the InnerProduct's output), staged in LDS, and leaves in 16-byte row
@@ -26,6 +28,7 @@
 // Every fp32 operation follows the unfused kernels' order without fused
 // multiply-adds, so the epilogue adds no rounding of its own.
 #include "sv2_internal.h"
+#include <climits>
 
 #pragma clang fp contract(off)
 
@@ -40,22 +43,17 @@ typedef __attribute__((ext_vector_type(16))) float f16acc;
 
 constexpr int kBM = 256;                      // rows of Y per workgroup
 constexpr int kBN = 256;                      // columns of Y (rows of W) per workgroup
-constexpr int kBK = 64;                       // K per stage
-constexpr int kStages = 2;                    // LDS stages (one in flight)
+constexpr int kBK = 64;                       // K per stage: whole 128-byte lines of every row
 constexpr int kKSteps = kBK / 16;             // MFMA k-steps per stage
 constexpr int kRowBytes = kBK * 2;            // 128
 constexpr int kTileBytes = kBM * kRowBytes;   // 32 KB: one operand tile of a stage
-constexpr int kStageBytes = 2 * kTileBytes;   // W tile + X tile
-constexpr int kThreads = 512;
+constexpr int kStageBytes = 2 * kTileBytes;   // 64 KB: W tile + X tile
+constexpr int kThreads = 256;                 // 4 waves, one per SIMD, 128 x 128 of Y each
 constexpr int kGroupM = 4;                    // row bands per tile group (see the tile order)
-constexpr int kEpiStride = 144;               // bytes per staged output row (128 + 16: bank spread)
-constexpr int kEpiBytes = 128 * kEpiStride;   // one wave's 128 x 64 fp16 block
-constexpr int kLds = (kStages * kStageBytes > 8 * kEpiBytes) ? kStages * kStageBytes : 8 * kEpiBytes;
+constexpr int kEpiStride = 272;               // bytes per staged output row (256 + 16: bank spread)
+constexpr int kEpiBytes = 128 * kEpiStride;   // one wave's 128 x 128 fp16 block
+constexpr int kLds = (2 * kStageBytes > 4 * kEpiBytes) ? 2 * kStageBytes : 4 * kEpiBytes;
 static_assert(kLds <= 160 * 1024, "LDS of one gfx950 CU");
-
-// s_waitcnt immediates: vmcnt(N) with expcnt / lgkmcnt unconstrained (gfx9
-// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
-constexpr int kWaitVm0 = 0x0F70;
 
 constexpr int kStore = kGemmStore;
 constexpr int kResidual = kGemmResidual;
@@ -67,53 +65,98 @@ struct GemmArgs
     const _Float16* w;  // [N][K]
     const _Float16* w2; // kSwiGLU: the value projection [N][K]
     _Float16* y;        // [M][N]
-    const _Float16* r; // kResidual: [M][N]
-    const float* bias; // [N] or null
-    const float* gate; // [N] or null
+    const _Float16* r;  // kResidual: [M][N]
+    const float* bias;  // [N] or null
+    const float* gate;  // [N] or null
     int m, n, k;
     int epi;
     int tiles_n;        // N / 256 (kSwiGLU: N / 128)
 };
 
-// Stage tiles are 256 rows of 128 bytes (64 fp16 of K); 16-byte chunk c
-// (k = 8c..8c+7) of row r sits in slot c ^ (r & 7), so the operand reads of
-// 8 consecutive rows hit all 32 banks.
-
-// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i
-// writes LDS bytes [lds + 16 i, lds + 16 i + 16), lds wave-uniform.  Inline
-// assembly keeps the compiler from waiting on it before unrelated LDS reads;
-// the loop places the vmcnt waits.  M0 is saved and restored.
-__device__ inline void dma16(const void* g, char* lds)
+// Global -> register -> LDS staging.  Lane l of wave w loads rows
+// 64 w + 8 i + l / 8 (i = 0..7) of the W tile and of the X tile, 16-byte
+// chunk l % 8 of the stage's 128 bytes, and writes it to slot
+// (l % 8) ^ (row % 8) of its row.  Buffer loads: the lane's part of the
+// offset is one VGPR per operand, the row and stage parts are uniform (SGPR
+// offset); X rows past M lie past the buffer's end and read as zero.
+struct Operands
 {
-    const unsigned base = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<size_t>(lds)));
-    unsigned saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "s"(base), "v"(g)
-                 : "memory");
+    __amdgpu_buffer_rsrc_t w;
+    __amdgpu_buffer_rsrc_t x;
+    int vw;   // lane's byte offset in W: (wrow0 + 64 wave + lane / 8) * 2K + 16 (lane % 8)
+    int vx;   // lane's byte offset in X: (m0 + 64 wave + lane / 8) * 2K + 16 (lane % 8)
+    int row8; // bytes of 8 rows: 16 K
+};
+
+struct StageRegs
+{
+    uint4 w[8];
+    uint4 x[8];
+};
+
+__device__ inline Operands make_operands(const GemmArgs& a, int m0, int wbase, int wave, int lane)
+{
+    Operands o;
+    const bool swiglu = a.epi == kSwiGLU;
+    const _Float16* wsrc = swiglu && wave >= 2 ? a.w2 : a.w;
+    const int wrow0 = swiglu ? wbase - 128 * (wave >> 1) : wbase;
+    o.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(wsrc), static_cast<short>(0), a.n * a.k * 2,
+                                            0x00020000);
+    o.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.x), static_cast<short>(0), a.m * a.k * 2,
+                                            0x00020000);
+    const int row = 64 * wave + (lane >> 3);
+    o.vw = (wrow0 + row) * a.k * 2 + 16 * (lane & 7);
+    o.vx = (m0 + row) * a.k * 2 + 16 * (lane & 7);
+    o.row8 = 16 * a.k;
+    return o;
 }
 
-// Stage kt of the workgroup's tile: wave w fetches rows 32w..32w+31 of the W
-// tile and of the X tile, 8 rows (1 KB) per instruction, lane l taking row
-// l / 8 of the 8 and the chunk that lands in slot l % 8 (8 fetches per lane).
-// W tile row r is row wbase + r of W, or for kSwiGLU row wbase + r % 128 of
-// W (r < 128, waves 0-3) or W2 (waves 4-7).  X rows past M repeat row M - 1
-// (their outputs are not stored).
-__device__ inline void fetch_stage(const GemmArgs& a, char* stage, int m0, int wbase, int kt, int wave, int lane)
+__device__ inline void load_stage(const Operands& o, StageRegs& r, int kt)
 {
-    const int k0 = kt * kBK;
-    const bool swiglu = a.epi == kSwiGLU;
-    const _Float16* wsrc = swiglu && wave >= 4 ? a.w2 : a.w;
-    const int wrow0 = swiglu ? wbase - 128 * (wave >> 2) : wbase;
+    const int k0 = kt * kRowBytes;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++)
     {
-        const int r0 = 32 * wave + 8 * i;
-        const int r = r0 + (lane >> 3);
-        const int c = (lane & 7) ^ (r & 7);
-        dma16(wsrc + static_cast<long long>(wrow0 + r) * a.k + k0 + 8 * c, stage + r0 * kRowBytes);
-        const int xr = min(m0 + r, a.m - 1);
-        dma16(a.x + static_cast<long long>(xr) * a.k + k0 + 8 * c, stage + kTileBytes + r0 * kRowBytes);
+        const int so = __builtin_amdgcn_readfirstlane(i * o.row8 + k0);
+        r.w[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(o.w, o.vw, so, 0));
+        r.x[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(o.x, o.vx, so, 0));
+    }
+}
+
+__device__ inline void store_stage(const StageRegs& r, char* stage, int wave, int lane)
+{
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+    {
+        const int row = 64 * wave + 8 * i + (lane >> 3);
+        const int off = row * kRowBytes + (((lane & 7) ^ (row & 7)) << 4);
+        *reinterpret_cast<uint4*>(stage + off) = r.w[i];
+        *reinterpret_cast<uint4*>(stage + kTileBytes + off) = r.x[i];
+    }
+}
+
+// part p of a stage: the lane's W and X rows of groups i = 2p, 2p + 1
+__device__ inline void load_part(const Operands& o, StageRegs& r, int kt, int p)
+{
+    const int k0 = kt * kRowBytes;
+#pragma unroll
+    for (int i = 2 * p; i < 2 * p + 2; i++)
+    {
+        const int so = __builtin_amdgcn_readfirstlane(i * o.row8 + k0);
+        r.w[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(o.w, o.vw, so, 0));
+        r.x[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(o.x, o.vx, so, 0));
+    }
+}
+
+__device__ inline void store_part(const StageRegs& r, char* stage, int wave, int lane, int p)
+{
+#pragma unroll
+    for (int i = 2 * p; i < 2 * p + 2; i++)
+    {
+        const int row = 64 * wave + 8 * i + (lane >> 3);
+        const int off = row * kRowBytes + (((lane & 7) ^ (row & 7)) << 4);
+        *reinterpret_cast<uint4*>(stage + off) = r.w[i];
+        *reinterpret_cast<uint4*>(stage + kTileBytes + off) = r.x[i];
     }
 }
 
@@ -122,8 +165,6 @@ __device__ inline float h2f(_Float16 v)
     return static_cast<float>(v);
 }
 
-// Per-column epilogue operands of a lane's 8 output columns (the same for
-// every row the lane stores): bias and gate, read once.
 struct EpiCols
 {
     float b[8];
@@ -153,13 +194,11 @@ __device__ inline EpiCols epi_cols(const GemmArgs& a, int col)
     return c;
 }
 
-// Epilogue of one 16-byte segment (8 columns) of an output row.
 __device__ inline h8 finish_segment(const GemmArgs& a, const EpiCols& c, const h8 p, long long row, int col)
 {
     h8 out;
     if (a.epi == kStore)
         return p;
-    // kResidual
     const h8 res = *reinterpret_cast<const h8*>(a.r + row * a.n + col);
 #pragma unroll
     for (int e = 0; e < 8; e++)
@@ -180,11 +219,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31;
     const int g = lane >> 5;
-    const int wm = wave >> 2; // 128-row half of the tile (X rows)
-    const int wn = wave & 3;  // 64-column quarter (W rows)
+    const int wm = wave >> 1; // 128-row half of the tile (X rows)
+    const int wn = wave & 1;  // 128-column half (W rows)
 
     // workgroup ids go round-robin over the 8 XCDs; each XCD takes a
     // contiguous run of tiles (whole row bands, sharing their X rows in the
@@ -207,10 +246,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
     const int tn = in_group / group_rows;
     const int m0 = tm * kBM;
     const bool swiglu = a.epi == kSwiGLU;
-    const int n0 = swiglu ? tn * 128 : tn * kBN; // first Y column of the tile, first W row fetched
+    const int n0 = swiglu ? tn * 128 : tn * kBN;
     const int nk = a.k / kBK;
 
-    // per-lane operand offsets: row 64 * wn (W) / 128 * wm (X) + lr of a
+    // per-lane operand offsets: row 128 * wn (W) / 128 * wm (X) + lr of a
     // tile, chunk 2 ks + g; the 32-row blocks add 4096 bytes each
     const int swz = lr & 7;
     int offw[kKSteps];
@@ -218,71 +257,114 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ks++)
     {
-        offw[ks] = (64 * wn + lr) * kRowBytes + (((2 * ks + g) ^ swz) << 4);
+        offw[ks] = (128 * wn + lr) * kRowBytes + (((2 * ks + g) ^ swz) << 4);
         offx[ks] = kTileBytes + (128 * wm + lr) * kRowBytes + (((2 * ks + g) ^ swz) << 4);
     }
 
-    f16acc acc[4][2];
+    f16acc acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
             acc[i][j] = f16acc{};
 
-#pragma unroll
-    for (int s = 0; s < kStages - 1; s++)
-        if (s < nk)
-            fetch_stage(a, smem + s * kStageBytes, m0, n0, s, wave, lane);
+    const Operands ops = make_operands(a, m0, n0, wave, lane);
+    // Stage s: loaded into register set s % 2 two iterations ahead, written
+    // to LDS slot s % 2 in four parts (part 0 after the barrier of iteration
+    // s - 2, parts 1-3 during the first three k-steps of iteration s - 1,
+    // each part's registers reloaded with stage s + 2 right after), read
+    // after the barrier of iteration s - 1.  Every iteration writes and
+    // loads (stages past the last load stage nk - 1 again and are never
+    // multiplied), so the loop body has no branches and the compiler's waits
+    // for the loads are exact.
+    StageRegs ra, rb;
+    const int last = nk - 1;
+    load_stage(ops, ra, 0);
+    load_stage(ops, rb, min(1, last));
+    store_stage(ra, smem, wave, lane);
+    load_stage(ops, ra, min(2, last));
+    store_part(rb, smem + kStageBytes, wave, lane, 0);
+    load_part(ops, rb, min(3, last), 0);
+    __syncthreads();
 
-    for (int kt = 0; kt < nk; kt++)
-    {
-        // stage kt, the only one in flight, has landed; after the barrier
-        // every wave's part is visible and every wave has finished reading
-        // stage kt - 1, whose buffer the fetch of stage kt + 1 reuses
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        __syncthreads();
-        if (kt + kStages - 1 < nk)
-            fetch_stage(a, smem + ((kt + kStages - 1) % kStages) * kStageBytes, m0, n0, kt + kStages - 1, wave,
-                        lane);
-        const char* st = smem + (kt % kStages) * kStageBytes;
-        // the operands of two k-steps are read at a time (12 reads), pinned
-        // ahead of their MFMAs: left to itself the scheduler reads each
-        // operand right before its MFMAs and waits for it
+    h8 fw[2][4], fx[2][4];
+    auto read_ops = [&](h8 (&w4)[4], h8 (&x4)[4], const char* st, int ks) {
 #pragma unroll
-        for (int kp = 0; kp < kKSteps; kp += 2)
+        for (int b = 0; b < 4; b++)
         {
-            h8 fw[2][2];
-            h8 fx[2][4];
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-            {
-#pragma unroll
-                for (int b = 0; b < 2; b++)
-                    fw[h][b] = *reinterpret_cast<const h8*>(st + offw[kp + h] + b * 4096);
-#pragma unroll
-                for (int b = 0; b < 4; b++)
-                    fx[h][b] = *reinterpret_cast<const h8*>(st + offx[kp + h] + b * 4096);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[h][j], fx[h][i], acc[i][j], 0, 0, 0);
+            w4[b] = *reinterpret_cast<const h8*>(st + offw[ks] + b * 4096);
+            x4[b] = *reinterpret_cast<const h8*>(st + offx[ks] + b * 4096);
         }
+    };
+    auto mfmas = [&](const h8 (&w4)[4], const h8 (&x4)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w4[j], x4[i], acc[i][j], 0, 0, 0);
+    };
+    // scheduling groups (masks: 0x100 LDS read, 0x008 MFMA, 0x200 LDS write,
+    // 0x020 global read): a phase's eight operand reads first, then its 16
+    // MFMAs in groups of four, each group's first MFMA followed by one write
+    // and one load
+    auto interleave = [&]() {
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+        {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+        }
+    };
+    read_ops(fw[0], fx[0], smem, 0);
+
+    // Iteration kt (stage kt in slot kt % 2, its k-step 0 operands in
+    // fw/fx[0]; `nx` holds stage kt + 1's parts 1-3, `cur` stage kt + 2):
+    // k-steps 0-2 each with the next k-step's reads and one part of stage
+    // kt + 1; the barrier (the slot's reads are done, stage kt + 1 is
+    // visible); k-step 3 with stage kt + 1's first reads and part 0 of stage
+    // kt + 2 into this slot.
+    auto iter = [&](int kt, StageRegs& cur, StageRegs& nx) {
+        char* st = smem + (kt & 1) * kStageBytes;
+        char* sn = smem + ((kt + 1) & 1) * kStageBytes;
+#pragma unroll
+        for (int ks = 0; ks < kKSteps - 1; ks++)
+        {
+            read_ops(fw[(ks + 1) & 1], fx[(ks + 1) & 1], st, ks + 1);
+            mfmas(fw[ks & 1], fx[ks & 1]);
+            store_part(nx, sn, wave, lane, ks + 1);
+            load_part(ops, nx, min(kt + 3, last), ks + 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+        read_ops(fw[0], fx[0], sn, 0);
+        mfmas(fw[1], fx[1]);
+        store_part(cur, st, wave, lane, 0);
+        load_part(ops, cur, min(kt + 4, last), 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2)
+    {
+        iter(kt, ra, rb);
+        iter(kt + 1, rb, ra);
     }
+    if (kt < nk)
+        iter(kt, ra, rb);
 
     // acc[i][j] register 4q + e holds Y row m0 + 128 wm + 32 i + lr, column
-    // n0 + 64 wn + 32 j + 8 q + 4 g + e.  Round to fp16 (the InnerProduct's
-    // output) and stage the wave's 128 x 64 block row-major in LDS.
-    __syncthreads(); // every wave is done with the stage buffers
+    // n0 + 128 wn + 32 j + 8 q + 4 g + e.
+    __syncthreads();
     char* mine = smem + wave * kEpiBytes;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++)
             {
@@ -295,21 +377,17 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
 
     if (swiglu)
     {
-        // the gate columns 64 c..64 c + 63 of the tile sit in the block of
-        // wave (wm, c), the matching value columns in wave (wm, c + 2); wave
-        // (wm, wn) writes rows 64 (wn >> 1)..+63 of the 128-row half wm,
-        // columns n0 + 64 c.. with c = wn & 1
+        // gate block: wave (wm, 0), value block: wave (wm, 1); wave (wm, wn)
+        // writes rows 64 wn..64 wn + 63 of the 128-row half wm
         __syncthreads();
-        const int c = wn & 1;
-        const char* gate_blk = smem + (4 * wm + c) * kEpiBytes;
-        const char* val_blk = smem + (4 * wm + c + 2) * kEpiBytes;
-        const int chunk = lane & 7;
-        const int ycol = n0 + 64 * c + 8 * chunk;
-        const int ncols = a.n;
+        const char* gate_blk = smem + (2 * wm) * kEpiBytes;
+        const char* val_blk = smem + (2 * wm + 1) * kEpiBytes;
+        const int chunk = lane & 15;
+        const int ycol = n0 + 8 * chunk;
 #pragma unroll 4
-        for (int it = 0; it < 8; it++)
+        for (int it = 0; it < 16; it++)
         {
-            const int rl = 64 * (wn >> 1) + 8 * it + (lane >> 3);
+            const int rl = 64 * wn + 4 * it + (lane >> 4);
             const long long row = m0 + 128 * wm + rl;
             if (row >= a.m)
                 continue;
@@ -323,23 +401,20 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
                 const float den = 1.f + expf(-gf);
                 out[e] = static_cast<_Float16>((gf / den) * h2f(uv[e]));
             }
-            *reinterpret_cast<h8*>(a.y + row * ncols + ycol) = out;
+            *reinterpret_cast<h8*>(a.y + row * a.n + ycol) = out;
         }
         return;
     }
 
-    // the block was written and is read back by this wave only: LDS
-    // operations of a wave complete in order, the wait keeps the compiler
-    // from reordering them
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
-    const int chunk = lane & 7;
-    const int col = n0 + 64 * wn + 8 * chunk;
+    const int chunk = lane & 15;
+    const int col = n0 + 128 * wn + 8 * chunk;
     const EpiCols ec = epi_cols(a, col);
 #pragma unroll 4
-    for (int it = 0; it < 16; it++)
+    for (int it = 0; it < 32; it++)
     {
-        const int rl = 8 * it + (lane >> 3);
+        const int rl = 4 * it + (lane >> 4);
         const long long row = m0 + 128 * wm + rl;
         if (row >= a.m)
             continue;
@@ -347,7 +422,6 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(GemmArgs a)
         *reinterpret_cast<h8*>(a.y + row * a.n + col) = finish_segment(a, ec, p, row, col);
     }
 }
-
 } // namespace
 
 bool gemm_mfma_supported(int in, int out, int epi)
@@ -369,6 +443,9 @@ int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, cons
                          "inner product: needs in a multiple of 64 and out a multiple of 256 (SwiGLU: 128)");
     if (!x || !w || !y || (epi == kResidual && !residual) || (epi == kSwiGLU && !w2))
         return set_error(SV2_EINVAL, "inner product: null pointer");
+    // the operands are read through buffer resources with 32-bit byte offsets
+    if (static_cast<long long>(rows) * in * 2 > INT_MAX || static_cast<long long>(out) * in * 2 > INT_MAX)
+        return set_error(SV2_EUNSUPPORTED, "inner product: an operand exceeds 2 GiB");
     const int rc = set_dynamic_lds(reinterpret_cast<const void*>(&gemm_f16_kernel), kLds,
                                    "gemm_mfma: dynamic LDS attribute");
     if (rc != SV2_OK)
