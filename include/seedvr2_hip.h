@@ -159,7 +159,7 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream);
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc); it has no counterpart in the reference.  args->workspace
  * and workspace_bytes are ignored: the scratch is a static device array of
- * the library, 48 MiB per device (the 720p x 21f workload needs 43.7 MB), held
+ * the library, 48 MiB per device (the 720p x 21f workload needs 44.3 MB), held
  * until the process ends.  Calls whose sv2_window_attention_workspace exceeds
  * it, and the exact mode, return SV2_EUNSUPPORTED.  Calls that overlap on one
  * device share the array and race; calls on one stream are ordered.

@@ -134,7 +134,9 @@ def test_attention_argument_checks(hip):
 
 
 def test_workspace_size_formula(hip):
-    """Per-window bf16 text partials plus the prepared text q, k and v^T."""
+    """Per-window bf16 text partials, the prepared text q, k and v^T, and the
+    first two text tiles' v^T per head in the attention kernel's LDS byte
+    order."""
     lib = hip.load()
     a = hip.AttnArgs()
     a.rule = hip.rule(6, 45, 80, True, 2, 9, 16)
@@ -147,7 +149,7 @@ def test_workspace_size_formula(hip):
 
     def al(x):
         return (x + 255) // 256 * 256
-    expect = al(144 * 58 * D * 2) + al(20 * 58 * 128 * 2) * 2 + al(20 * 128 * 64 * 2)
+    expect = al(144 * 58 * D * 2) + al(20 * 58 * 128 * 2) * 2 + al(20 * 128 * 64 * 2) + al(20 * 2 * 64 * 128 * 2)
     assert got == expect
     a.text_len = 0
     assert lib.sv2_window_attention_workspace(ctypes.byref(a)) == 0
