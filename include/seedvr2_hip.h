@@ -19,9 +19,10 @@
  *     stream) and never synchronise;
  *   - return codes: SV2_OK (0), SV2_EINVAL (-1, bad argument, the reference's
  *     invalid-input code), SV2_EUNSUPPORTED (-2, valid but unsupported shape),
- *     SV2_EDEVICE (-100, a HIP error, the reference's allocation/sublayer
- *     failure code).  sv2_last_error() returns a message for the last failure
- *     on the calling thread.
+ *     SV2_EDEVICE (-100, a HIP error or a failed host allocation, the
+ *     reference's allocation/sublayer failure code).  sv2_last_error()
+ *     returns a message for the last failure on the calling thread.  No C++
+ *     exception leaves an entry point.
  */
 #ifndef SEEDVR2_HIP_H
 #define SEEDVR2_HIP_H

@@ -2285,9 +2285,10 @@ int launch_exact(const AttnParams& p, const Workspace& w, char* base, int rope_m
 } // namespace
 
 // Scratch of the no-allocation entry point (sv2_window_attention_no_alloc):
-// the per-window bf16 text partials and the prepared text q, k, v^T of one
-// attention call.  48 MiB covers the 720p x 21f workload (144 windows x 58
-// text tokens x 2560 channels of partials, 43.7 MB in all).  Each device that
+// the per-window bf16 text partials, the prepared text q, k, v^T and the
+// first text tiles' v^T in LDS order of one attention call.  48 MiB covers the
+// 720p x 21f workload (144 windows x 58 text tokens x 2560 channels of
+// partials, 44.3 MB in all).  Each device that
 // loads the library holds its own copy until the process ends.  Every byte a
 // call reads is written earlier in the same call (all text rows of every
 // window and head, the whole prepared text), so nothing is cleared between
@@ -2339,6 +2340,7 @@ int attention_captures(const sv2_attn_args* args, float* q, float* k, float* v, 
 extern "C" {
 
 int64_t sv2_window_attention_workspace(const sv2_attn_args* args)
+try
 {
     using namespace sv2;
     AttnParams p;
@@ -2348,8 +2350,13 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args)
         return rc;
     return workspace_layout(p).total;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_window_attention_workspace");
+}
 
 int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
+try
 {
     using namespace sv2;
     AttnParams p;
@@ -2389,8 +2396,13 @@ int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
     }
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_window_attention");
+}
 
 int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!args)
@@ -2417,8 +2429,13 @@ int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream_ptr)
     a.workspace_bytes = static_cast<size_t>(kStaticScratchBytes);
     return sv2_window_attention(&a, stream_ptr);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_window_attention_no_alloc");
+}
 
 int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float* v_out, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!args)
@@ -2428,8 +2445,13 @@ int sv2_qk_prologue(const sv2_attn_args* args, float* q_out, float* k_out, float
     return run_prologue(args, PrologueOut{q_out, k_out, v_out, nullptr, nullptr}, nullptr, nullptr,
                         static_cast<hipStream_t>(stream_ptr));
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_qk_prologue");
+}
 
 int sv2_window_index_map(const sv2_window_rule* rule, int32_t* out, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!rule || !out)
@@ -2444,6 +2466,10 @@ int sv2_window_index_map(const sv2_window_rule* rule, int32_t* out, void* stream
     if (err != hipSuccess)
         return hip_error(err, "window_index_map_kernel launch");
     return SV2_OK;
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_window_index_map");
 }
 
 } // extern "C"

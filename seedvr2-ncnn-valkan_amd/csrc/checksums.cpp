@@ -219,6 +219,7 @@ int parse_manifest(const std::string& path, std::vector<Entry>* out)
 extern "C" {
 
 int sv2_sha256(const void* data, size_t bytes, unsigned char digest[32])
+try
 {
     if ((!data && bytes) || !digest)
         return sv2::set_error(SV2_EINVAL, "sv2_sha256: null argument");
@@ -227,16 +228,26 @@ int sv2_sha256(const void* data, size_t bytes, unsigned char digest[32])
     s.finish(digest);
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_sha256");
+}
 
 int sv2_sha256_file(const char* path, unsigned char digest[32])
+try
 {
     if (!path || !digest)
         return sv2::set_error(SV2_EINVAL, "sv2_sha256_file: null argument");
     return sv2::hash_file(path, digest) ? SV2_OK
                                         : sv2::set_error(SV2_EINVAL, std::string("sv2_sha256_file: cannot read ") + path);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_sha256_file");
+}
 
 int sv2_verify_checksums(const char* dir, int threads)
+try
 {
     using namespace sv2;
     if (!dir)
@@ -280,6 +291,10 @@ int sv2_verify_checksums(const char* dir, int threads)
             return set_error(SV2_EINVAL, std::string("checksums: ") + root + "/" + entries[i].name +
                                              (status[i] == 1 ? " is missing or unreadable" : " is corrupted (SHA256 mismatch)"));
     return static_cast<int>(entries.size());
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_verify_checksums");
 }
 
 } // extern "C"

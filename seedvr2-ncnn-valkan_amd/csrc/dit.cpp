@@ -222,6 +222,7 @@ extern "C" {
 
 int sv2_dit_input_create(const sv2_dit_input_config* config, const sv2_dit_input_weights* w, int weights_on_device,
                          int compute_dtype, sv2_dit_input** out)
+try
 {
     using namespace sv2;
     if (!config || !w || !out)
@@ -295,8 +296,13 @@ int sv2_dit_input_create(const sv2_dit_input_config* config, const sv2_dit_input
     *out = in;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_input_create");
+}
 
 int sv2_dit_input_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_dit_input** out)
+try
 {
     using namespace sv2;
     if (!param_path || !bin_path || !out)
@@ -346,25 +352,40 @@ int sv2_dit_input_load(const char* param_path, const char* bin_path, int compute
     w.b_time_out = biases[4].data();
     return sv2_dit_input_create(&c, &w, 0, compute_dtype, out);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_input_load");
+}
 
 int sv2_dit_input_get_config(const sv2_dit_input* head, sv2_dit_input_config* config)
+try
 {
     if (!head || !config)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_input_get_config: null argument");
     *config = head->cfg;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_input_get_config");
+}
 
 int64_t sv2_dit_input_workspace_size(const sv2_dit_input* head, int frames, int height, int width, int text_len)
+try
 {
     if (!head || frames <= 0 || height <= 0 || width <= 0 || height % 2 != 0 || width % 2 != 0 || text_len < 0)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_input_workspace_size: bad argument");
     return static_cast<int64_t>(input_layout(head, frames, height, width, text_len).total);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_input_workspace_size");
+}
 
 int sv2_dit_input_forward(sv2_dit_input* in, const float* video, int channel_major, const float* text, int text_len,
                           float timestep, int frames, int height, int width, void* vid_out, void* txt_out, float* emb,
                           void* workspace, size_t workspace_bytes, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!in || !video || !vid_out || !emb || text_len < 0 || (text_len > 0 && (!text || !txt_out)))
@@ -421,6 +442,10 @@ int sv2_dit_input_forward(sv2_dit_input* in, const float* video, int channel_maj
         return rc;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_input_forward");
+}
 
 void sv2_dit_input_destroy(sv2_dit_input* head)
 {
@@ -429,6 +454,7 @@ void sv2_dit_input_destroy(sv2_dit_input* head)
 
 int sv2_dit_output_create(const sv2_dit_output_config* config, const sv2_dit_output_weights* w,
                           int weights_on_device, int compute_dtype, sv2_dit_output** out)
+try
 {
     using namespace sv2;
     if (!config || !w || !out)
@@ -473,8 +499,13 @@ int sv2_dit_output_create(const sv2_dit_output_config* config, const sv2_dit_out
     *out = o;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_output_create");
+}
 
 int sv2_dit_output_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_dit_output** out)
+try
 {
     using namespace sv2;
     if (!param_path || !bin_path || !out)
@@ -513,25 +544,40 @@ int sv2_dit_output_load(const char* param_path, const char* bin_path, int comput
     w.b_proj = bp.data();
     return sv2_dit_output_create(&c, &w, 0, compute_dtype, out);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_output_load");
+}
 
 int sv2_dit_output_get_config(const sv2_dit_output* head, sv2_dit_output_config* config)
+try
 {
     if (!head || !config)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_output_get_config: null argument");
     *config = head->cfg;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_output_get_config");
+}
 
 int64_t sv2_dit_output_workspace_size(const sv2_dit_output* head, int frames, int height, int width)
+try
 {
     if (!head || frames <= 0 || height <= 0 || width <= 0)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_output_workspace_size: bad argument");
     return static_cast<int64_t>(output_layout(head, frames, height, width).total);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_output_workspace_size");
+}
 
 int sv2_dit_output_forward(sv2_dit_output* o, const void* vid, const float* emb, int frames, int height, int width,
                            float* output, int channel_major, void* workspace, size_t workspace_bytes,
                            void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!o || !vid || !emb || !output)
@@ -567,6 +613,10 @@ int sv2_dit_output_forward(sv2_dit_output* o, const void* vid, const float* emb,
         return rc;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_output_forward");
+}
 
 void sv2_dit_output_destroy(sv2_dit_output* head)
 {
@@ -575,6 +625,7 @@ void sv2_dit_output_destroy(sv2_dit_output* head)
 
 int sv2_dit_create(sv2_dit_input* input, sv2_block* const* blocks, int block_count, sv2_dit_output* output,
                    sv2_dit** out)
+try
 {
     using namespace sv2;
     if (!input || !output || !out || block_count < 0 || (block_count > 0 && !blocks))
@@ -601,8 +652,13 @@ int sv2_dit_create(sv2_dit_input* input, sv2_block* const* blocks, int block_cou
     *out = d;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_create");
+}
 
 int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out)
+try
 {
     using namespace sv2;
     if (!model_dir || !out)
@@ -655,6 +711,10 @@ int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out)
     }
     *out = d;
     return SV2_OK;
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_load");
 }
 
 } // extern "C"
@@ -710,6 +770,7 @@ extern "C" {
 
 int sv2_dit_get_config(const sv2_dit* dit, sv2_dit_input_config* input, sv2_dit_output_config* output,
                        int* block_count)
+try
 {
     if (!dit)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_get_config: null dit");
@@ -721,8 +782,13 @@ int sv2_dit_get_config(const sv2_dit* dit, sv2_dit_input_config* input, sv2_dit_
         *block_count = static_cast<int>(dit->blocks.size());
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_get_config");
+}
 
 int64_t sv2_dit_workspace_size(sv2_dit* dit, int frames, int height, int width, int text_len)
+try
 {
     if (!dit)
         return sv2::set_error(SV2_EINVAL, "sv2_dit_workspace_size: null dit");
@@ -730,9 +796,14 @@ int64_t sv2_dit_workspace_size(sv2_dit* dit, int frames, int height, int width, 
     const int rc = dit_layout(dit, frames, height, width, text_len, &lay);
     return rc == SV2_OK ? static_cast<int64_t>(lay.total) : rc;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_workspace_size");
+}
 
 int sv2_dit_forward(sv2_dit* d, const float* latent, const float* text, int text_len, float timestep, int frames,
                     int height, int width, float* output, void* workspace, size_t workspace_bytes, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!d || !latent || !output || text_len < 0 || (text_len > 0 && !text))
@@ -771,6 +842,10 @@ int sv2_dit_forward(sv2_dit* d, const float* latent, const float* text, int text
         cur ^= 1;
     }
     return sv2_dit_output_forward(d->output, vid[cur], emb, frames, h, w, output, 1, scratch, scratch_bytes, stream);
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_dit_forward");
 }
 
 void sv2_dit_destroy(sv2_dit* dit)

@@ -401,6 +401,7 @@ void sv2_block_config_default(sv2_block_config* c)
 
 int sv2_block_create(const sv2_block_config* config, const sv2_block_branch* vid, const sv2_block_branch* txt,
                      const float* rope_freqs, int weights_on_device, int compute_dtype, sv2_block** out)
+try
 {
     using namespace sv2;
     if (!config || !vid || !out || (!config->shared_weights && !txt))
@@ -431,8 +432,13 @@ int sv2_block_create(const sv2_block_config* config, const sv2_block_branch* vid
     *out = b;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_create");
+}
 
 int sv2_block_load(const char* param_path, const char* bin_path, int compute_dtype, sv2_block** out)
+try
 {
     using namespace sv2;
     if (!param_path || !bin_path || !out)
@@ -520,16 +526,26 @@ int sv2_block_load(const char* param_path, const char* bin_path, int compute_dty
     const sv2_block_branch tb = view(hb[nbranch - 1]);
     return sv2_block_create(&c, &vb, &tb, freqs.data(), 0, compute_dtype, out);
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_load");
+}
 
 int sv2_block_get_config(const sv2_block* block, sv2_block_config* config)
+try
 {
     if (!block || !config)
         return sv2::set_error(SV2_EINVAL, "sv2_block_get_config: null argument");
     *config = block->cfg;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_get_config");
+}
 
 int sv2_block_set_runtime_shape(sv2_block* block, int frames, int height, int width)
+try
 {
     if (!block)
         return sv2::set_error(SV2_EINVAL, "sv2_block_set_runtime_shape: null block");
@@ -539,8 +555,13 @@ int sv2_block_set_runtime_shape(sv2_block* block, int frames, int height, int wi
     block->shape_valid = frames > 0 && height > 0 && width > 0;
     return block->shape_valid ? SV2_OK : sv2::set_error(SV2_EINVAL, "sv2_block_set_runtime_shape: bad shape");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_set_runtime_shape");
+}
 
 int64_t sv2_block_workspace_size(const sv2_block* block, int text_len)
+try
 {
     using namespace sv2;
     if (!block || text_len < 0)
@@ -551,9 +572,14 @@ int64_t sv2_block_workspace_size(const sv2_block* block, int text_len)
     const int rc = workspace_layout(block, text_len, &w);
     return rc == SV2_OK ? static_cast<int64_t>(w.total) : rc;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_workspace_size");
+}
 
 int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_len, const float* emb, void* vid_out,
                       void* txt_out, void* workspace, size_t workspace_bytes, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!b || !vid || !emb || !vid_out || text_len < 0 || (text_len > 0 && (!txt || !txt_out)))
@@ -785,8 +811,13 @@ int sv2_block_forward(sv2_block* b, const void* vid, const void* txt, int text_l
         return rc;
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_forward");
+}
 
 int64_t sv2_block_window_rows(const sv2_block* block, int text_len)
+try
 {
     using namespace sv2;
     if (!block || text_len < 0)
@@ -805,9 +836,14 @@ int64_t sv2_block_window_rows(const sv2_block* block, int text_len)
         rows += int64_t(w.t1 - w.t0) * (w.h1 - w.h0) * (w.w1 - w.w0) + text_len;
     return rows;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_window_rows");
+}
 
 int sv2_block_forward_host(sv2_block* b, const float* vid, const float* txt, int text_len, const float* emb,
                            float* vid_out, float* txt_out, const sv2_block_debug* host_debug)
+try
 {
     using namespace sv2;
     if (!b || !vid || !emb || !vid_out || text_len < 0 || (text_len > 0 && (!txt || !txt_out)))
@@ -924,8 +960,13 @@ int sv2_block_forward_host(sv2_block* b, const float* vid, const float* txt, int
         err = hipMemcpy(caps[i].host, dev(caps[i].offset), size_t(caps[i].count) * 4, hipMemcpyDeviceToHost);
     return err == hipSuccess ? SV2_OK : hip_error(err, "sv2_block_forward_host: download");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_forward_host");
+}
 
 int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug)
+try
 {
     if (!block)
         return sv2::set_error(SV2_EINVAL, "sv2_block_set_debug: null block");
@@ -933,6 +974,10 @@ int sv2_block_set_debug(sv2_block* block, const sv2_block_debug* debug)
     if (debug)
         block->debug = *debug;
     return SV2_OK;
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_block_set_debug");
 }
 
 void sv2_block_destroy(sv2_block* block)

@@ -566,6 +566,7 @@ extern "C" {
 
 int sv2_rmsnorm_ada(const void* x, void* y, int io_dtype, int rows, int dim, float eps, const float* emb,
                     const float* shift, const float* scale, int slot_base, int has_ada, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!dtype_ok(io_dtype) || rows < 0 || dim <= 0)
@@ -581,9 +582,14 @@ int sv2_rmsnorm_ada(const void* x, void* y, int io_dtype, int rows, int dim, flo
     const EmbInput mod{emb, shift, scale, slot_base};
     return launch_rmsnorm(x, y, io_dtype, rows, dim, eps, mod, nullptr, has_ada, static_cast<hipStream_t>(stream_ptr));
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_rmsnorm_ada");
+}
 
 int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int dim, const float* emb,
                      const float* gate_vec, int slot_base, int mode, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!dtype_ok(io_dtype) || rows < 0 || dim <= 0 || mode < 0 || mode > 2)
@@ -599,8 +605,13 @@ int sv2_ada_residual(void* x, const void* residual, int io_dtype, int rows, int 
     const EmbGate gate{emb, gate_vec, slot_base + 2};
     return launch_residual(x, residual, io_dtype, rows, dim, gate, nullptr, mode, static_cast<hipStream_t>(stream_ptr));
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_ada_residual");
+}
 
 int sv2_swiglu(void* gate, const void* value, int io_dtype, int64_t count, void* stream_ptr)
+try
 {
     using namespace sv2;
     if (!dtype_ok(io_dtype) || count < 0)
@@ -621,6 +632,10 @@ int sv2_swiglu(void* gate, const void* value, int io_dtype, int64_t count, void*
         hipLaunchKernelGGL(swiglu_kernel<BF16>, grid, dim3(256), 0, stream, gate, value, static_cast<long long>(count));
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? SV2_OK : hip_error(err, "swiglu_kernel launch");
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_swiglu");
 }
 
 } // extern "C"

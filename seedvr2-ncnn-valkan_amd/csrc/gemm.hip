@@ -476,6 +476,7 @@ int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, cons
 extern "C" int sv2_inner_product_f16(const void* x, const void* w, const void* w_value, void* y, int rows, int in,
                                      int out, int epilogue, const float* bias, const float* gate,
                                      const void* residual, void* stream)
+try
 {
     static_assert(SV2_EPI_STORE == sv2::kGemmStore && SV2_EPI_RESIDUAL == sv2::kGemmResidual &&
                       SV2_EPI_SWIGLU == sv2::kGemmSwiGLU,
@@ -484,5 +485,9 @@ extern "C" int sv2_inner_product_f16(const void* x, const void* w, const void* w
         return sv2::set_error(SV2_EINVAL, "sv2_inner_product_f16: w_value is only read by SV2_EPI_SWIGLU");
     return sv2::gemm_mfma(static_cast<hipStream_t>(stream), rows, in, out, x, w, w_value, y, epilogue, bias, gate,
                           residual);
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_inner_product_f16");
 }
 

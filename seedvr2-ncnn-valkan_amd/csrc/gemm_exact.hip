@@ -239,6 +239,11 @@ int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x
 
 extern "C" int sv2_inner_product_f32(const float* x, const float* w, const float* bias, float* y, int rows, int in,
                                      int out, void* stream)
+try
 {
     return sv2::gemm_f32_exact(static_cast<hipStream_t>(stream), rows, in, out, x, w, bias, y);
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_inner_product_f32");
 }

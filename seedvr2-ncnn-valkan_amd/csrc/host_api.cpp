@@ -5,6 +5,8 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <utility>
 #include <vector>
@@ -105,6 +107,35 @@ int set_error(int code, const std::string& message)
     return code;
 }
 
+int caught_exception(const char* entry) noexcept
+{
+    std::string what;
+    try
+    {
+        throw;
+    }
+    catch (const std::bad_alloc&)
+    {
+        what = "out of host memory";
+    }
+    catch (const std::exception& e)
+    {
+        what = e.what();
+    }
+    catch (...)
+    {
+        what = "unknown exception";
+    }
+    try
+    {
+        return set_error(SV2_EDEVICE, std::string(entry) + ": " + what);
+    }
+    catch (...)
+    {
+        return SV2_EDEVICE; // no memory left even for the message
+    }
+}
+
 int hip_error(hipError_t err, const char* what)
 {
     char buffer[256];
@@ -161,6 +192,7 @@ int build_plan(const sv2_window_rule& rule, PlanArgs* plan)
 extern "C" {
 
 int sv2_window_plan(const sv2_window_rule* rule, sv2_window* out, int cap)
+try
 {
     using namespace sv2;
     if (!rule || cap < 0 || (cap > 0 && !out))
@@ -182,6 +214,10 @@ int sv2_window_plan(const sv2_window_rule* rule, sv2_window* out, int cap)
     }
     return plan.nwin;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_window_plan");
+}
 
 size_t sv2_rope_table_floats(int npos)
 {
@@ -189,6 +225,7 @@ size_t sv2_rope_table_floats(int npos)
 }
 
 int sv2_rope_table_build(int rope_mode, const float* freqs, float theta, int npos, float* host_table)
+try
 {
     using namespace sv2;
     if (npos <= 0 || !host_table)
@@ -243,8 +280,13 @@ int sv2_rope_table_build(int rope_mode, const float* freqs, float theta, int npo
             }
     return SV2_OK;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_rope_table_build");
+}
 
 int sv2_rope_positions_needed(const sv2_window_rule* rule, int text_len, int rope_mode)
+try
 {
     using namespace sv2;
     if (!rule || text_len < 0)
@@ -266,6 +308,10 @@ int sv2_rope_positions_needed(const sv2_window_rule* rule, int text_len, int rop
         max_w = std::max(max_w, plan.w.b[i + 1] - plan.w.b[i]);
     // video positions (L_txt + t_local, y_local, x_local); text (l, l, l)
     return std::max(std::max(text_len + max_t, text_len), std::max(max_h, max_w));
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_rope_positions_needed");
 }
 
 const char* sv2_last_error(void)

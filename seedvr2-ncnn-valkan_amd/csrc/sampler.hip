@@ -203,6 +203,7 @@ int check_count(long long count, const char* what)
 extern "C" {
 
 int sv2_euler_timesteps(int steps, float* out)
+try
 {
     if (!out)
         return sv2::set_error(SV2_EINVAL, "sv2_euler_timesteps: null output");
@@ -211,6 +212,10 @@ int sv2_euler_timesteps(int steps, float* out)
     for (int i = 0; i < n; i++)
         out[i] = 1000.0f * (1.0f - static_cast<float>(i) / n);
     return n;
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_euler_timesteps");
 }
 
 float sv2_condition_ratio(float noise_scale, int frames, int height, int width)
@@ -233,6 +238,7 @@ float sv2_condition_ratio(float noise_scale, int frames, int height, int width)
 
 int sv2_make_condition(const float* encoded, const float* noise, float* out, int64_t count, float ratio,
                        void* stream)
+try
 {
     using namespace sv2;
     int rc = check_count(count, "sv2_make_condition");
@@ -246,9 +252,14 @@ int sv2_make_condition(const float* encoded, const float* noise, float* out, int
                        encoded, noise, out, static_cast<long long>(count), ratio);
     return launch_status("condition_kernel launch");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_make_condition");
+}
 
 int sv2_make_dit_input(const float* latent, const float* condition, float* out, int64_t tokens, int channel_major,
                        void* stream)
+try
 {
     using namespace sv2;
     int rc = check_count(33 * tokens, "sv2_make_dit_input");
@@ -263,16 +274,26 @@ int sv2_make_dit_input(const float* latent, const float* condition, float* out, 
                        channel_major ? 1 : 0);
     return launch_status("dit_input_kernel launch");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_make_dit_input");
+}
 
 int64_t sv2_cfg_workspace_size(int64_t count)
+try
 {
     (void)count;
     // partial sums of every reduction block + the factor
     return static_cast<int64_t>(sv2::kReduceBlocks) * 4 * sizeof(double) + 256;
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_cfg_workspace_size");
+}
 
 int sv2_apply_cfg(const float* positive, const float* negative, float* out, int64_t count, float scale,
                   float rescale, void* workspace, size_t workspace_bytes, void* stream_ptr)
+try
 {
     using namespace sv2;
     int rc = check_count(count, "sv2_apply_cfg");
@@ -307,9 +328,14 @@ int sv2_apply_cfg(const float* positive, const float* negative, float* out, int6
                        static_cast<long long>(count), factor);
     return launch_status("cfg_scale_kernel launch");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_apply_cfg");
+}
 
 int sv2_euler_step(const float* prediction, const float* current, float* out, int64_t count, float timestep,
                    float next_timestep, void* stream)
+try
 {
     using namespace sv2;
     int rc = check_count(count, "sv2_euler_step");
@@ -328,9 +354,14 @@ int sv2_euler_step(const float* prediction, const float* current, float* out, in
                        prediction, current, out, static_cast<long long>(count), bt, at, as, bs, 0);
     return launch_status("euler_kernel launch");
 }
+catch (...)
+{
+    return sv2::caught_exception("sv2_euler_step");
+}
 
 int sv2_euler_endpoint(const float* prediction, const float* current, float* out, int64_t count, float timestep,
                        void* stream)
+try
 {
     using namespace sv2;
     int rc = check_count(count, "sv2_euler_endpoint");
@@ -345,6 +376,10 @@ int sv2_euler_endpoint(const float* prediction, const float* current, float* out
     hipLaunchKernelGGL(euler_kernel, dim3(blocks_for(count)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                        prediction, current, out, static_cast<long long>(count), bt, 0.0f, 1.0f, 0.0f, 1);
     return launch_status("euler_kernel launch");
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_euler_endpoint");
 }
 
 } // extern "C"

@@ -102,6 +102,11 @@ __host__ __device__ inline float bf16_round(float value)
 // Thread-local error message plumbing for the C ABI.
 int set_error(int code, const std::string& message);
 int hip_error(hipError_t err, const char* what);
+// Called from the catch clause of an entry point of the C ABI, which lets no
+// C++ exception out (std::bad_alloc of a host container, std::system_error
+// of a thread): records what was caught and returns SV2_EDEVICE, the
+// allocation-failure code.
+int caught_exception(const char* entry) noexcept;
 // Raises a kernel's dynamic LDS limit to at least `bytes` on the current
 // device.  The attribute is per device; it is set once per (kernel, device)
 // and size, under a lock, not on every launch.

@@ -127,3 +127,39 @@ def test_dit_load_refuses_a_bad_manifest(hip, tmp_path):
     with pytest.raises(hip.Sv2Error) as err:
         hip.Dit.load(d, hip.F16)
     assert "seedvr2_dit_block_17.ncnn.bin is corrupted" in str(err.value), str(err.value)
+
+
+_OOM_CHILD = r"""
+import ctypes, resource, sys
+sys.path.insert(0, sys.argv[1])
+import sv2hip
+lib = sv2hip.load()
+digest = (ctypes.c_ubyte * 32)()
+# every mapping from here on fails: the 4 MiB read buffer cannot be allocated
+with open("/proc/self/statm") as f:
+    pages = int(f.read().split()[0])
+size = pages * resource.getpagesize()
+resource.setrlimit(resource.RLIMIT_AS, (size + (1 << 20), resource.RLIM_INFINITY))
+rc = lib.sv2_sha256_file(sys.argv[2].encode(), digest)
+resource.setrlimit(resource.RLIMIT_AS, (resource.RLIM_INFINITY, resource.RLIM_INFINITY))
+print(rc, lib.sv2_last_error().decode())
+"""
+
+
+def test_out_of_host_memory_is_an_error_code(hip, tmp_path):
+    """No C++ exception leaves the C ABI: a host allocation that fails inside
+    an entry point (here the read buffer of sv2_sha256_file, in a child
+    process whose address space is capped) comes back as SV2_EDEVICE, the
+    reference's allocation-failure code, with a message."""
+    import os
+    import subprocess
+    import sys
+    path = tmp_path / "data.bin"
+    path.write_bytes(b"x" * 1000)
+    pkg = os.path.dirname(hip.__file__)
+    out = subprocess.run([sys.executable, "-c", _OOM_CHILD, pkg, str(path)], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr[-2000:]
+    rc, msg = out.stdout.strip().split(" ", 1)
+    assert int(rc) == hip.SV2_EDEVICE
+    assert "sv2_sha256_file" in msg and "out of host memory" in msg
