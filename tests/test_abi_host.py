@@ -172,3 +172,32 @@ def test_elementwise_argument_checks(hip):
     assert lib.sv2_swiglu(16, 16, hip.F16, 12, None) == hip.SV2_EUNSUPPORTED
     assert lib.sv2_swiglu(None, 16, hip.F16, 16, None) == hip.SV2_EINVAL
     assert lib.sv2_swiglu(None, None, hip.F16, 0, None) == hip.SV2_OK
+
+
+def test_inner_product_argument_checks(hip):
+    """Shape, pointer and size checks of the InnerProduct entry points return
+    before any launch: the hand-written fp16 product needs in % 64 == 0 and
+    out % 256 == 0 (SwiGLU: % 128), and refuses operands past 2 GiB (its
+    buffer resources take 32-bit byte offsets); the fp32 exact product needs
+    positive sizes."""
+    lib = hip.load()
+    p = 16  # a non-null dummy address: every case below returns before touching it
+    f16 = lib.sv2_inner_product_f16
+    assert f16(p, p, None, p, 4, 48, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EUNSUPPORTED
+    assert f16(p, p, None, p, 4, 64, 200, hip.EPI_STORE, None, None, None, None) == hip.SV2_EUNSUPPORTED
+    assert f16(p, p, p, p, 4, 64, 192, hip.EPI_SWIGLU, None, None, None, None) == hip.SV2_EUNSUPPORTED
+    assert f16(p, p, None, p, 4, 64, 256, 7, None, None, None, None) == hip.SV2_EINVAL
+    assert f16(None, p, None, p, 4, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EINVAL
+    assert f16(p, p, None, p, 4, 64, 256, hip.EPI_RESIDUAL, None, None, None, None) == hip.SV2_EINVAL
+    assert f16(p, p, None, p, 4, 64, 256, hip.EPI_SWIGLU, None, None, None, None) == hip.SV2_EINVAL
+    assert f16(p, p, p, p, 4, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EINVAL
+    # 2^24 rows x 64 in x 2 B = 2 GiB of X; 65536 outputs x 16384 in x 2 B = 2 GiB of W
+    assert f16(p, p, None, p, 1 << 24, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EUNSUPPORTED
+    assert "2 GiB" in lib.sv2_last_error().decode()
+    assert f16(p, p, None, p, 4, 16384, 65536, hip.EPI_STORE, None, None, None, None) == hip.SV2_EUNSUPPORTED
+    assert f16(None, None, None, None, 0, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_OK
+    f32 = lib.sv2_inner_product_f32
+    assert f32(p, p, None, p, 4, 0, 16, None) == hip.SV2_EINVAL
+    assert f32(p, p, None, p, -1, 16, 16, None) == hip.SV2_EINVAL
+    assert f32(None, p, None, p, 4, 16, 16, None) == hip.SV2_EINVAL
+    assert f32(None, None, None, None, 0, 16, 16, None) == hip.SV2_OK
