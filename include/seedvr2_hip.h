@@ -297,6 +297,14 @@ int sv2_block_forward(sv2_block* block, const void* vid, const void* txt, int te
 
 void sv2_block_destroy(sv2_block* block);
 
+/* Host.  A diagnostic with no counterpart in the reference: 1 when the last
+ * sv2_block_forward ran its row-wise steps (RMSNorm + ada, the InnerProducts,
+ * gated residuals, SwiGLU) once over the video and text rows together (shared
+ * weights outside the last layer, no debug captures, text rows right after the
+ * video rows in the caller's buffers and in the workspace), 0 when it ran
+ * them per branch, a negative error code for a null block. */
+int sv2_block_last_forward_merged(const sv2_block* block);
+
 /* Host.  Rows of the window-sequence order at the current runtime shape:
  * the sum over the windows of (window video tokens + text_len), the row
  * count of the attention_q/k/v/output captures (seedvr2_dit_block.cpp:
@@ -449,6 +457,13 @@ typedef struct sv2_dit sv2_dit;
  * first (sv2_verify_checksums) and a failed check fails the load with
  * SV2_EINVAL before any weight is read. */
 int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out);
+/* sv2_dit_load with the check chosen: SV2_VERIFY_NONE hashes nothing (the
+ * reference's loader, src/model/dit.cpp:120-174, never does; about 7 GB of
+ * hashing is saved), SV2_VERIFY_IF_PRESENT is sv2_dit_load, SV2_VERIFY_STRICT
+ * also fails without a SHA256SUMS (sv2_verify_checksums_strict).  The check
+ * reads the files in a pass of its own before the load reads them. */
+enum sv2_verify_mode { SV2_VERIFY_NONE = 0, SV2_VERIFY_IF_PRESENT = 1, SV2_VERIFY_STRICT = 2 };
+int sv2_dit_load_ex(const char* model_dir, int compute_dtype, int verify, sv2_dit** out);
 /* Assembles a DiT from existing heads and blocks (borrowed; they must outlive
  * the DiT and share its compute dtype). */
 int sv2_dit_create(sv2_dit_input* input, sv2_block* const* blocks, int block_count, sv2_dit_output* output,
@@ -571,6 +586,21 @@ int sv2_sha256_file(const char* path, unsigned char digest[32]);
  * SV2_EINVAL for a malformed manifest, a listed file that is missing, or a
  * digest that does not match (sv2_last_error names the line or file). */
 int sv2_verify_checksums(const char* dir, int threads);
+
+/* sv2_verify_checksums, but a directory without a non-empty SHA256SUMS fails
+ * with SV2_EINVAL, as scripts/verify-models.sh:22 fails a component without
+ * one.  A file that cannot be hashed for lack of host memory gives
+ * SV2_EDEVICE (both functions). */
+int sv2_verify_checksums_strict(const char* dir, int threads);
+
+/* scripts/verify-models.sh for the parts this library loads: under
+ * `model_root`, default_pos_emb.bin and default_neg_emb.bin present and, when
+ * `bundled_embeddings` is not NULL, byte-identical to the copies in that
+ * directory (:27-31); dit_full_fp16/SHA256SUMS required and every listed file
+ * intact (:33-34); all 68 files of the DiT present and non-empty (:36-47).
+ * The VAE component is not checked (the library has no VAE).  Returns the
+ * number of DiT files hashed, or a negative error code naming the file. */
+int sv2_verify_model_set(const char* model_root, const char* bundled_embeddings, int threads);
 
 const char* sv2_last_error(void);
 

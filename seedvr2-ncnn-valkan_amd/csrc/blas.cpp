@@ -12,7 +12,9 @@
 // (per-channel alpha, beta 1, optional bias), planned per shape in the same
 // way.
 // fp32 (the parity mode): gemm_f32_exact (gemm_exact.hip), double
-// accumulation in the order of the CPU restatement, the bias added in double.
+// accumulation in the order of the CPU oracle, the bias added in double; bit
+// for bit the oracle's W x + b, and against ncnn's float InnerProduct (whose
+// summation order is unknown here) equal only up to its rounding.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>

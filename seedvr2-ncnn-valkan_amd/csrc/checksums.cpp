@@ -216,6 +216,114 @@ int parse_manifest(const std::string& path, std::vector<Entry>* out)
 } // namespace
 } // namespace sv2
 
+namespace sv2
+{
+namespace
+{
+
+// Size of a file in bytes, -1 when it cannot be opened.
+long long file_size(const std::string& path)
+{
+    std::FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f)
+        return -1;
+    long long n = -1;
+    if (std::fseek(f, 0, SEEK_END) == 0)
+        n = std::ftell(f);
+    std::fclose(f);
+    return n;
+}
+
+bool read_whole(const std::string& path, std::vector<unsigned char>* out)
+{
+    std::FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f)
+        return false;
+    out->clear();
+    unsigned char buf[1 << 16];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof(buf), f)) > 0)
+        out->insert(out->end(), buf, buf + n);
+    const bool ok = !std::ferror(f);
+    std::fclose(f);
+    return ok;
+}
+
+// `sha256sum --check --strict SHA256SUMS` in `dir`.  Without a manifest:
+// 0 (nothing to check), or an error when `strict` (scripts/verify-models.sh:22
+// requires a non-empty one).  Each worker records per file 0 (ok), 1
+// (unreadable), 2 (mismatch) or 3 (could not be hashed: an allocation failed
+// on its thread), so no exception leaves a thread; when a thread cannot be
+// started the threads already running and the calling thread share the
+// files, and every started thread is joined before returning.
+int verify_manifest(const std::string& root, int threads, bool strict)
+{
+    const std::string manifest = root + "/SHA256SUMS";
+    const long long size = file_size(manifest);
+    if (size < 0 || (strict && size == 0))
+    {
+        if (strict)
+            return set_error(SV2_EINVAL, "checksums: " + manifest + " is missing");
+        return 0; // nothing to check
+    }
+    std::vector<Entry> entries;
+    int rc = parse_manifest(manifest, &entries);
+    if (rc != SV2_OK)
+        return rc;
+    if (threads <= 0)
+        threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
+    threads = std::min<int>(threads, static_cast<int>(entries.size()));
+    // each worker takes the next file; the first failure in list order is reported
+    std::atomic<size_t> next{0};
+    std::vector<int> status(entries.size(), 0);
+    auto work = [&]() noexcept {
+        for (size_t i; (i = next.fetch_add(1)) < entries.size();)
+        {
+            try
+            {
+                unsigned char digest[32];
+                if (!hash_file(root + "/" + entries[i].name, digest))
+                    status[i] = 1;
+                else if (hex(digest) != entries[i].digest)
+                    status[i] = 2;
+            }
+            catch (...)
+            {
+                status[i] = 3;
+            }
+        }
+    };
+    std::vector<std::thread> pool;
+    try
+    {
+        pool.reserve(static_cast<size_t>(threads));
+        for (int t = 1; t < threads; t++)
+            pool.emplace_back(work);
+    }
+    catch (...)
+    {
+        // fewer threads than asked for: the rest of the files go to the
+        // threads already started and to this one
+    }
+    work();
+    for (std::thread& t : pool)
+        t.join();
+    for (size_t i = 0; i < entries.size(); i++)
+    {
+        if (status[i] == 3)
+            return set_error(SV2_EDEVICE, "checksums: " + root + "/" + entries[i].name +
+                                              " could not be hashed (out of host memory)");
+        if (status[i])
+            return set_error(SV2_EINVAL, "checksums: " + root + "/" + entries[i].name +
+                                             (status[i] == 1 ? " is missing or unreadable"
+                                                             : " is corrupted (SHA256 mismatch)"));
+    }
+    return static_cast<int>(entries.size());
+}
+
+} // namespace
+} // namespace sv2
+
 extern "C" {
 
 int sv2_sha256(const void* data, size_t bytes, unsigned char digest[32])
@@ -249,52 +357,72 @@ catch (...)
 int sv2_verify_checksums(const char* dir, int threads)
 try
 {
-    using namespace sv2;
     if (!dir)
-        return set_error(SV2_EINVAL, "sv2_verify_checksums: null directory");
-    const std::string root(dir);
-    const std::string manifest = root + "/SHA256SUMS";
-    {
-        std::FILE* f = std::fopen(manifest.c_str(), "rb");
-        if (!f)
-            return 0; // nothing to check
-        std::fclose(f);
-    }
-    std::vector<Entry> entries;
-    int rc = parse_manifest(manifest, &entries);
-    if (rc != SV2_OK)
-        return rc;
-    if (threads <= 0)
-        threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
-    threads = std::min<int>(threads, static_cast<int>(entries.size()));
-    // each worker takes the next file; the first failure in list order is reported
-    std::atomic<size_t> next{0};
-    std::vector<int> status(entries.size(), 0); // 0 ok, 1 unreadable, 2 mismatch
-    auto work = [&]() {
-        for (size_t i; (i = next.fetch_add(1)) < entries.size();)
-        {
-            unsigned char digest[32];
-            if (!hash_file(root + "/" + entries[i].name, digest))
-                status[i] = 1;
-            else if (hex(digest) != entries[i].digest)
-                status[i] = 2;
-        }
-    };
-    std::vector<std::thread> pool;
-    for (int t = 1; t < threads; t++)
-        pool.emplace_back(work);
-    work();
-    for (std::thread& t : pool)
-        t.join();
-    for (size_t i = 0; i < entries.size(); i++)
-        if (status[i])
-            return set_error(SV2_EINVAL, std::string("checksums: ") + root + "/" + entries[i].name +
-                                             (status[i] == 1 ? " is missing or unreadable" : " is corrupted (SHA256 mismatch)"));
-    return static_cast<int>(entries.size());
+        return sv2::set_error(SV2_EINVAL, "sv2_verify_checksums: null directory");
+    return sv2::verify_manifest(dir, threads, false);
 }
 catch (...)
 {
     return sv2::caught_exception("sv2_verify_checksums");
+}
+
+int sv2_verify_checksums_strict(const char* dir, int threads)
+try
+{
+    if (!dir)
+        return sv2::set_error(SV2_EINVAL, "sv2_verify_checksums_strict: null directory");
+    return sv2::verify_manifest(dir, threads, true);
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_verify_checksums_strict");
+}
+
+int sv2_verify_model_set(const char* model_root, const char* bundled_embeddings, int threads)
+try
+{
+    using namespace sv2;
+    if (!model_root)
+        return set_error(SV2_EINVAL, "sv2_verify_model_set: null model directory");
+    const std::string root(model_root);
+    // the default text embeddings: present, and equal to the bundled ones
+    // (scripts/verify-models.sh:27-31)
+    for (const char* name : {"default_pos_emb.bin", "default_neg_emb.bin"})
+    {
+        std::vector<unsigned char> have;
+        if (!read_whole(root + "/" + name, &have) || have.empty())
+            return set_error(SV2_EINVAL, std::string("model set: ") + name + " is missing");
+        if (bundled_embeddings)
+        {
+            std::vector<unsigned char> want;
+            if (!read_whole(std::string(bundled_embeddings) + "/" + name, &want))
+                return set_error(SV2_EINVAL, std::string("model set: the bundled ") + name + " is missing");
+            if (have != want)
+                return set_error(SV2_EINVAL, std::string("model set: ") + name + " differs from the bundled embedding");
+        }
+    }
+    // the DiT component: its manifest required and every listed file intact
+    // (:33-34), then every file the DiT loads present and non-empty (:36-47)
+    const std::string dit = root + "/dit_full_fp16";
+    const int n = verify_manifest(dit, threads, true);
+    if (n < 0)
+        return n;
+    std::vector<std::string> stems = {"seedvr2_dit_input", "seedvr2_dit_output"};
+    for (int i = 0; i < 32; i++)
+    {
+        char stem[64];
+        std::snprintf(stem, sizeof(stem), "seedvr2_dit_block_%02d", i);
+        stems.push_back(stem);
+    }
+    for (const std::string& stem : stems)
+        for (const char* ext : {".ncnn.param", ".ncnn.bin"})
+            if (file_size(dit + "/" + stem + ext) <= 0)
+                return set_error(SV2_EINVAL, "model set: dit_full_fp16/" + stem + ext + " is missing or empty");
+    return n;
+}
+catch (...)
+{
+    return sv2::caught_exception("sv2_verify_model_set");
 }
 
 } // extern "C"

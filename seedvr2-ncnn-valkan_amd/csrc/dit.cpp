@@ -658,11 +658,18 @@ catch (...)
 }
 
 int sv2_dit_load(const char* model_dir, int compute_dtype, sv2_dit** out)
+{
+    return sv2_dit_load_ex(model_dir, compute_dtype, SV2_VERIFY_IF_PRESENT, out);
+}
+
+int sv2_dit_load_ex(const char* model_dir, int compute_dtype, int verify, sv2_dit** out)
 try
 {
     using namespace sv2;
     if (!model_dir || !out)
         return set_error(SV2_EINVAL, "sv2_dit_load: null argument");
+    if (verify < SV2_VERIFY_NONE || verify > SV2_VERIFY_STRICT)
+        return set_error(SV2_EINVAL, "sv2_dit_load: unknown verify mode");
     *out = nullptr;
     const std::string root(model_dir);
     auto path = [&](const std::string& stem, const char* ext) { return root + "/" + stem + ".ncnn" + ext; };
@@ -682,8 +689,11 @@ try
                 return set_error(SV2_EINVAL, "sv2_dit_load: DiT model file is missing: " + path(s, ext));
             std::fclose(f);
         }
-    // the directory's SHA256SUMS, when it has one (scripts/verify-models.sh:17-24)
-    const int checked = sv2_verify_checksums(model_dir, 0);
+    // the directory's SHA256SUMS (scripts/verify-models.sh:17-24): when it
+    // has one, or required
+    const int checked = verify == SV2_VERIFY_NONE     ? 0
+                        : verify == SV2_VERIFY_STRICT ? sv2_verify_checksums_strict(model_dir, 0)
+                                                      : sv2_verify_checksums(model_dir, 0);
     if (checked < 0)
         return checked;
     sv2_dit* d = new sv2_dit();

@@ -54,15 +54,21 @@ struct sv2_block
     bool has_freqs = false;
     int T = 0, H = 0, W = 0;
     bool shape_valid = false;
-    // RoPE table cache for the current rule and text length
+    // RoPE cos/sin table on the device, covering rope_npos positions; grown
+    // only.  Tables it replaced (queued work may still read them) and the
+    // pinned host copies of every upload stay allocated until the block goes.
     float* rope = nullptr;
     int rope_npos = 0;
-    int rope_key[5] = {-1, -1, -1, -1, -1};
+    std::vector<float*> rope_retired;
+    std::vector<float*> rope_host;
     // workspace kept by the block when the caller passes none
     void* ws = nullptr;
     size_t ws_bytes = 0;
     bool debug_on = false;
     sv2_block_debug debug{};
+    // whether the last forward ran the row-wise steps over the video and
+    // text rows at once (sv2_block_last_forward_merged)
+    int last_merged = 0;
     // device staging of sv2_block_forward_host, grown on demand
     void* stage = nullptr;
     size_t stage_bytes = 0;
@@ -75,6 +81,10 @@ struct sv2_block
             (void)hipFree(p);
         if (rope)
             (void)hipFree(rope);
+        for (float* t : rope_retired)
+            (void)hipFree(t);
+        for (float* h : rope_host)
+            (void)hipHostFree(h);
         if (ws)
             (void)hipFree(ws);
     }
@@ -172,49 +182,49 @@ sv2_window_rule block_rule(const sv2_block* b)
     return r;
 }
 
-// Builds (once per rule and text length) the RoPE cos/sin table on the device.
+// Makes the block's RoPE table cover the positions this forward needs.  A
+// position's row depends only on the rope mode and the block's frequencies,
+// and the attention indexes the table with the table's own position count,
+// so a table built for more positions serves every smaller need: CFG
+// forwards that alternate text lengths reuse it.  Growing enqueues the upload
+// of a pinned host copy into a new buffer and retires the old one; nothing
+// waits for the stream, so a forward whose table already covers its shape
+// launches kernels only (and can be captured in a HIP graph).
 int ensure_rope(sv2_block* b, int text_len, hipStream_t stream)
 {
     if (b->cfg.rope_mode == SV2_ROPE_NONE)
-        return SV2_OK;
-    const int key[5] = {b->T, b->H, b->W, b->cfg.shifted_window, text_len};
-    if (b->rope && std::equal(key, key + 5, b->rope_key))
         return SV2_OK;
     const sv2_window_rule rule = block_rule(b);
     const int npos = sv2_rope_positions_needed(&rule, text_len, b->cfg.rope_mode);
     if (npos < 0)
         return npos;
+    if (b->rope && npos <= b->rope_npos)
+        return SV2_OK;
     if (b->cfg.rope_mode == SV2_ROPE_REFERENCE && !b->has_freqs)
         return sv2::set_error(SV2_EINVAL, "block: the reference RoPE needs rope_freqs");
-    std::vector<float> table(sv2_rope_table_floats(npos));
-    int rc = sv2_rope_table_build(b->cfg.rope_mode, b->freqs, 10000.f, npos, table.data());
+    const size_t floats = sv2_rope_table_floats(npos);
+    float* host = nullptr;
+    hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&host), floats * sizeof(float), hipHostMallocDefault);
+    if (err != hipSuccess || !host)
+        return sv2::hip_error(err != hipSuccess ? err : hipErrorOutOfMemory, "block: pinned RoPE table");
+    b->rope_host.push_back(host);
+    int rc = sv2_rope_table_build(b->cfg.rope_mode, b->freqs, 10000.f, npos, host);
     if (rc != SV2_OK)
         return rc;
-    if (b->rope && npos > b->rope_npos)
-    {
-        // the previous table may still be read by queued work
-        hipError_t err = hipStreamSynchronize(stream);
-        if (err != hipSuccess)
-            return sv2::hip_error(err, "block: synchronize before RoPE table resize");
-        (void)hipFree(b->rope);
-        b->rope = nullptr;
-    }
-    if (!b->rope)
-    {
-        hipError_t err = hipMalloc(reinterpret_cast<void**>(&b->rope), table.size() * sizeof(float));
-        if (err != hipSuccess)
-        {
-            b->rope = nullptr;
-            return sv2::hip_error(err, "block: hipMalloc of the RoPE table");
-        }
-        b->rope_npos = npos;
-    }
-    hipError_t err = hipMemcpyAsync(b->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice, stream);
-    if (err == hipSuccess)
-        err = hipStreamSynchronize(stream); // the host table goes out of scope
+    float* dev = nullptr;
+    err = hipMalloc(reinterpret_cast<void**>(&dev), floats * sizeof(float));
+    if (err != hipSuccess || !dev)
+        return sv2::hip_error(err != hipSuccess ? err : hipErrorOutOfMemory, "block: hipMalloc of the RoPE table");
+    err = hipMemcpyAsync(dev, host, floats * sizeof(float), hipMemcpyHostToDevice, stream);
     if (err != hipSuccess)
+    {
+        (void)hipFree(dev);
         return sv2::hip_error(err, "block: RoPE table upload");
-    std::copy(key, key + 5, b->rope_key);
+    }
+    if (b->rope)
+        b->rope_retired.push_back(b->rope);
+    b->rope = dev;
+    b->rope_npos = npos;
     return SV2_OK;
 }
 
@@ -664,6 +674,7 @@ try
                         qkv_t == qkv_v + 3 * Lv * row_bytes && att_t == att_v + Lv * row_bytes &&
                         p_t == p_v + Lv * row_bytes;
     const int Lr = merged ? Lv + Lt : Lv; // rows of the video branch's row-wise steps
+    b->last_merged = merged ? 1 : 0;
     if (Lt > 0 && !merged &&
         ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
          (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
@@ -814,6 +825,13 @@ try
 catch (...)
 {
     return sv2::caught_exception("sv2_block_forward");
+}
+
+int sv2_block_last_forward_merged(const sv2_block* block)
+{
+    if (!block)
+        return sv2::set_error(SV2_EINVAL, "sv2_block_last_forward_merged: null block");
+    return block->last_merged;
 }
 
 int64_t sv2_block_window_rows(const sv2_block* block, int text_len)

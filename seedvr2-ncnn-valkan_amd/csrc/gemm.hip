@@ -104,9 +104,14 @@ __device__ inline Operands make_operands(const GemmArgs& a, int m0, int wbase, i
                                             0x00020000);
     o.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.x), static_cast<short>(0), a.m * a.k * 2,
                                             0x00020000);
-    const int row = 64 * wave + (lane >> 3);
-    o.vw = (wrow0 + row) * a.k * 2 + 16 * (lane & 7);
-    o.vx = (m0 + row) * a.k * 2 + 16 * (lane & 7);
+    // byte offsets in 32-bit unsigned arithmetic: the rows of the last, padded
+    // X tile reach round_up(m, kBM) - 1, whose offset can pass INT_MAX when m *
+    // k * 2 is just under it; it stays below 2^32 (k < 2^22), and the buffer
+    // resource returns zeros for any offset past the operand
+    const uint32_t row = 64u * static_cast<uint32_t>(wave) + static_cast<uint32_t>(lane >> 3);
+    const uint32_t kb = 2u * static_cast<uint32_t>(a.k);
+    o.vw = static_cast<int>((static_cast<uint32_t>(wrow0) + row) * kb + 16u * static_cast<uint32_t>(lane & 7));
+    o.vx = static_cast<int>((static_cast<uint32_t>(m0) + row) * kb + 16u * static_cast<uint32_t>(lane & 7));
     o.row8 = 16 * a.k;
     return o;
 }
@@ -444,6 +449,8 @@ int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, cons
     if (!x || !w || !y || (epi == kResidual && !residual) || (epi == kSwiGLU && !w2))
         return set_error(SV2_EINVAL, "inner product: null pointer");
     // the operands are read through buffer resources with 32-bit byte offsets
+    // (the kernel forms them unsigned, so padded tile rows past `rows` stay
+    // exact; see make_operands)
     if (static_cast<long long>(rows) * in * 2 > INT_MAX || static_cast<long long>(out) * in * 2 > INT_MAX)
         return set_error(SV2_EUNSUPPORTED, "inner product: an operand exceeds 2 GiB");
     const int rc = set_dynamic_lds(reinterpret_cast<const void*>(&gemm_f16_kernel), kLds,

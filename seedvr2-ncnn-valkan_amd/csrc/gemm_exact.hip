@@ -5,8 +5,11 @@
 // The products of two floats are exact in double, so each step rounds only
 // the running sum, and the result is the same bit for bit as any evaluation
 // that adds the same exact products in the same order and rounds the same
-// way: the InnerProduct of ncnn (seedvr2_dit_block.cpp:28-56 creates it) as
-// the CPU restatement evaluates it, W [out][in] row-major, y = W x + b.
+// way: the CPU oracle's double-accumulated y = W x + b, W [out][in] row-major.
+// The reference's InnerProduct is ncnn's (seedvr2_dit_block.cpp:28-56 creates
+// it), which accumulates in float in an order not known here (ncnn is not in
+// the reference tree): against it this product is pinned by the closed form
+// y = W x + b only, not bit for bit.
 //
 // On the VALU in fp64 (an fp64 MFMA would sum four products per step in its
 // own order).  Two forms of the same arithmetic:

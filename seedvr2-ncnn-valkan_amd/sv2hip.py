@@ -22,6 +22,7 @@ SV2_EDEVICE = -100
 
 F32, F16, BF16 = 0, 1, 2
 ROPE_REFERENCE, ROPE_ABSOLUTE, ROPE_NONE = 0, 1, 2
+VERIFY_NONE, VERIFY_IF_PRESENT, VERIFY_STRICT = 0, 1, 2
 
 # Exported symbols declared in include/seedvr2_hip.h.
 EXPORTS = [
@@ -45,9 +46,12 @@ EXPORTS = [
     "sv2_block_workspace_size",
     "sv2_block_forward",
     "sv2_block_window_rows",
+    "sv2_block_last_forward_merged",
     "sv2_sha256",
     "sv2_sha256_file",
     "sv2_verify_checksums",
+    "sv2_verify_checksums_strict",
+    "sv2_verify_model_set",
     "sv2_block_forward_host",
     "sv2_block_destroy",
     "sv2_block_set_debug",
@@ -64,6 +68,7 @@ EXPORTS = [
     "sv2_dit_output_forward",
     "sv2_dit_output_destroy",
     "sv2_dit_load",
+    "sv2_dit_load_ex",
     "sv2_dit_create",
     "sv2_dit_get_config",
     "sv2_dit_workspace_size",
@@ -260,8 +265,14 @@ def load() -> ctypes.CDLL:
     lib.sv2_sha256_file.restype = i
     lib.sv2_verify_checksums.argtypes = [ctypes.c_char_p, i]
     lib.sv2_verify_checksums.restype = i
+    lib.sv2_verify_checksums_strict.argtypes = [ctypes.c_char_p, i]
+    lib.sv2_verify_checksums_strict.restype = i
+    lib.sv2_verify_model_set.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i]
+    lib.sv2_verify_model_set.restype = i
     lib.sv2_block_window_rows.argtypes = [vp, i]
     lib.sv2_block_window_rows.restype = ctypes.c_int64
+    lib.sv2_block_last_forward_merged.argtypes = [vp]
+    lib.sv2_block_last_forward_merged.restype = i
     lib.sv2_block_forward_host.argtypes = [vp, vp, vp, i, vp, vp, vp, vp]
     lib.sv2_block_forward_host.restype = i
     lib.sv2_block_set_debug.argtypes = [vp, ctypes.POINTER(BlockDebug)]
@@ -297,6 +308,8 @@ def load() -> ctypes.CDLL:
     lib.sv2_dit_output_destroy.restype = None
     lib.sv2_dit_load.argtypes = [ctypes.c_char_p, i, ctypes.POINTER(vp)]
     lib.sv2_dit_load.restype = i
+    lib.sv2_dit_load_ex.argtypes = [ctypes.c_char_p, i, i, ctypes.POINTER(vp)]
+    lib.sv2_dit_load_ex.restype = i
     lib.sv2_dit_create.argtypes = [vp, ctypes.POINTER(vp), i, vp, ctypes.POINTER(vp)]
     lib.sv2_dit_create.restype = i
     lib.sv2_dit_get_config.argtypes = [vp, ctypes.POINTER(DitInputConfig), ctypes.POINTER(DitOutputConfig),
@@ -593,6 +606,11 @@ class DitBlock:
         """Rows of the window-sequence order (attention_q/k/v/output captures)."""
         return check(load().sv2_block_window_rows(self._h, text_len), "sv2_block_window_rows")
 
+    def last_forward_merged(self) -> bool:
+        """Whether the last forward ran the row-wise steps over the video and
+        text rows at once."""
+        return bool(check(load().sv2_block_last_forward_merged(self._h), "sv2_block_last_forward_merged"))
+
     def forward(self, vid, txt, emb, vid_out, txt_out, workspace=None, stream=None):
         """vid [T*H*W, dim], txt [L, dim] (compute dtype), emb [6*dim] fp32."""
         self._check_blobs(vid, txt, emb, vid_out, txt_out)
@@ -836,9 +854,15 @@ class Dit(_Handle):
         self.output_channels = oc.output_channels
 
     @classmethod
-    def load(cls, model_dir, dtype=F32):
+    def load(cls, model_dir, dtype=F32, verify=None):
+        """sv2_dit_load (verify None: the manifest checked when present) or
+        sv2_dit_load_ex with VERIFY_NONE / VERIFY_IF_PRESENT / VERIFY_STRICT."""
         h = ctypes.c_void_p()
-        check(load().sv2_dit_load(str(model_dir).encode(), dtype, ctypes.byref(h)), "sv2_dit_load")
+        if verify is None:
+            check(load().sv2_dit_load(str(model_dir).encode(), dtype, ctypes.byref(h)), "sv2_dit_load")
+        else:
+            check(load().sv2_dit_load_ex(str(model_dir).encode(), dtype, verify, ctypes.byref(h)),
+                  "sv2_dit_load_ex")
         return cls(h.value, dtype)
 
     @classmethod
@@ -1039,3 +1063,17 @@ def verify_checksums(directory, threads: int = 0) -> int:
     """Checks `directory`/SHA256SUMS; returns the number of files verified (0
     when there is no manifest), raises Sv2Error on a failed check."""
     return check(load().sv2_verify_checksums(str(directory).encode(), threads), "sv2_verify_checksums")
+
+
+def verify_checksums_strict(directory, threads: int = 0) -> int:
+    """verify_checksums, but a directory without SHA256SUMS is an error."""
+    return check(load().sv2_verify_checksums_strict(str(directory).encode(), threads),
+                 "sv2_verify_checksums_strict")
+
+
+def verify_model_set(model_root, bundled_embeddings=None, threads: int = 0) -> int:
+    """The model-set check of scripts/verify-models.sh for the DiT (strict
+    manifest, the 68 DiT files, the default embeddings against the bundled
+    copies when a directory of them is given)."""
+    b = None if bundled_embeddings is None else str(bundled_embeddings).encode()
+    return check(load().sv2_verify_model_set(str(model_root).encode(), b, threads), "sv2_verify_model_set")

@@ -163,3 +163,105 @@ def test_out_of_host_memory_is_an_error_code(hip, tmp_path):
     rc, msg = out.stdout.strip().split(" ", 1)
     assert int(rc) == hip.SV2_EDEVICE
     assert "sv2_sha256_file" in msg and "out of host memory" in msg
+
+
+def test_strict_needs_a_manifest(hip, tmp_path):
+    d = _model_dir(tmp_path, FILES)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.verify_checksums_strict(d)
+    assert "SHA256SUMS is missing" in str(err.value)
+    (d / "SHA256SUMS").write_text("")
+    with pytest.raises(hip.Sv2Error):
+        hip.verify_checksums_strict(d)  # an empty manifest counts as missing (verify-models.sh:22, [ -s ... ])
+    (d / "SHA256SUMS").write_text(_manifest(FILES))
+    assert hip.verify_checksums_strict(d, 3) == len(FILES)
+
+
+DIT_NAMES = ["seedvr2_dit_input", "seedvr2_dit_output"] + [f"seedvr2_dit_block_{i:02d}" for i in range(32)]
+
+
+def _dit_dir(d):
+    files = {f"{n}.ncnn{ext}": f"{n}{ext}".encode() for n in DIT_NAMES for ext in (".param", ".bin")}
+    d.mkdir(parents=True, exist_ok=True)
+    _model_dir(d, files)
+    return files
+
+
+def test_dit_load_verify_modes(hip, tmp_path):
+    """sv2_dit_load_ex: VERIFY_STRICT refuses a directory without SHA256SUMS
+    and VERIFY_IF_PRESENT / VERIFY_STRICT a tampered file, all before any
+    weight is read; VERIFY_NONE skips the hashing and goes on to read the
+    (here not parseable) weights, failing there instead."""
+    files = _dit_dir(tmp_path)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.Dit.load(tmp_path, hip.F16, verify=hip.VERIFY_STRICT)
+    assert "SHA256SUMS is missing" in str(err.value)
+    (tmp_path / "SHA256SUMS").write_text(_manifest(files))
+    (tmp_path / "seedvr2_dit_block_05.ncnn.bin").write_bytes(b"tampered")
+    for mode in (hip.VERIFY_IF_PRESENT, hip.VERIFY_STRICT):
+        with pytest.raises(hip.Sv2Error) as err:
+            hip.Dit.load(tmp_path, hip.F16, verify=mode)
+        assert "seedvr2_dit_block_05.ncnn.bin is corrupted" in str(err.value)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.Dit.load(tmp_path, hip.F16, verify=hip.VERIFY_NONE)
+    assert "corrupted" not in str(err.value) and "SHA256" not in str(err.value), str(err.value)
+
+
+def test_model_set(hip, tmp_path):
+    """scripts/verify-models.sh for the DiT: embeddings present and equal to
+    the bundled copies, a strict dit_full_fp16 manifest, every DiT file."""
+    bundled = tmp_path / "bundled"
+    bundled.mkdir()
+    emb = {"default_pos_emb.bin": b"P" * 64, "default_neg_emb.bin": b"N" * 80}
+    _model_dir(bundled, emb)
+    root = tmp_path / "models"
+    files = _dit_dir(root / "dit_full_fp16")
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.verify_model_set(root, bundled)
+    assert "default_pos_emb.bin is missing" in str(err.value)
+    _model_dir(root, emb)
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.verify_model_set(root, bundled)
+    assert "SHA256SUMS is missing" in str(err.value)
+    (root / "dit_full_fp16" / "SHA256SUMS").write_text(_manifest(files))
+    assert hip.verify_model_set(root, bundled) == len(files)
+    assert hip.verify_model_set(root) == len(files)  # no bundled copies: presence only
+    (root / "default_neg_emb.bin").write_bytes(b"N" * 79 + b"X")
+    with pytest.raises(hip.Sv2Error) as err:
+        hip.verify_model_set(root, bundled)
+    assert "default_neg_emb.bin differs from the bundled embedding" in str(err.value)
+
+
+_THREAD_CHILD = r"""
+import ctypes, resource, sys
+sys.path.insert(0, sys.argv[1])
+import sv2hip
+lib = sv2hip.load()
+with open("/proc/self/statm") as f:
+    pages = int(f.read().split()[0])
+size = pages * resource.getpagesize()
+# no room for a thread stack nor a 4 MiB read buffer: starting the workers
+# and hashing both fail inside the call
+resource.setrlimit(resource.RLIMIT_AS, (size + (2 << 20), resource.RLIM_INFINITY))
+rc = lib.sv2_verify_checksums(sys.argv[2].encode(), 8)
+resource.setrlimit(resource.RLIMIT_AS, (resource.RLIM_INFINITY, resource.RLIM_INFINITY))
+print(rc, lib.sv2_last_error().decode())
+"""
+
+
+def test_checksum_workers_out_of_memory_is_an_error_code(hip, tmp_path):
+    """Threads that cannot start and hashes that cannot allocate inside
+    sv2_verify_checksums come back as an error code (a child process with its
+    address space capped), not as a terminated process."""
+    import os
+    import subprocess
+    import sys
+    d = _model_dir(tmp_path, FILES)
+    (d / "SHA256SUMS").write_text(_manifest(FILES))
+    pkg = os.path.dirname(hip.__file__)
+    out = subprocess.run([sys.executable, "-c", _THREAD_CHILD, pkg, str(d)], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, (out.returncode, out.stderr[-2000:])
+    rc, msg = out.stdout.strip().split(" ", 1)
+    assert int(rc) == hip.SV2_EDEVICE, (rc, msg)
+    assert "could not be hashed" in msg or "out of host memory" in msg, msg

@@ -520,8 +520,19 @@ def test_shared_block_rows_merged(hip, orc, device, dtype, grid, L, shifted):
         rows_in = torch.from_numpy(np.concatenate([vid, txt])).to(device=device, dtype=td)
         rows_out = torch.full_like(rows_in, float("nan"))
         blk.forward(rows_in[:Lv], rows_in[Lv:], e, rows_out[:Lv], rows_out[Lv:])
-        sep_v, sep_t = run_gpu(hip, blk, vid, txt, emb, T, H, W, device)
+        # the comparison below is only meaningful if this forward did merge
+        assert blk.last_forward_merged()
+        # the same rows with a one-row gap between video and text (separately
+        # allocated tensors may land next to each other and merge after all)
+        gap_in = torch.full((Lv + 1 + L, dim), float("nan"), dtype=td, device=device)
+        gap_in[:Lv] = rows_in[:Lv]
+        gap_in[Lv + 1:] = rows_in[Lv:]
+        gap_out = torch.full_like(gap_in, float("nan"))
+        blk.forward(gap_in[:Lv], gap_in[Lv + 1:], e, gap_out[:Lv], gap_out[Lv + 1:])
+        assert not blk.last_forward_merged()
         torch.cuda.synchronize()
+        sep_v = gap_out[:Lv].float().cpu().numpy()
+        sep_t = gap_out[Lv + 1:].float().cpu().numpy()
         mv, mt = (t.float().cpu().numpy() for t in (rows_out[:Lv], rows_out[Lv:]))
     finally:
         blk.close()
@@ -565,3 +576,28 @@ def test_forward_host_equals_device_forward(hip, device):
             assert np.array_equal(cap.view(np.uint32), dcap.cpu().numpy().view(np.uint32))
     finally:
         blk.close()
+
+
+def test_rows_not_merged_for_last_layer_or_captures(hip, device):
+    """The merged row-wise path is off for the last layer (its text rows skip
+    the ada input and gate, seedvr2_dit_block.cpp:1141-1151) and while debug
+    captures are set, even with the text rows right after the video rows."""
+    dim, heads, hidden, T, H, W, L = 256, 2, 512, 2, 4, 6, 5
+    rng = np.random.default_rng(41)
+    w = nf.random_weights(rng, dim, hidden, shared=True)
+    rows = torch.randn((T * H * W + L, dim), device=device)
+    out = torch.empty_like(rows)
+    e = torch.randn((6 * dim,), device=device)
+    Lv = T * H * W
+    for last, capture in ((0, False), (1, False), (0, True)):
+        cfg = hip.block_config(dim=dim, heads=heads, mlp_hidden=hidden, shared_weights=1, last_layer=last)
+        blk = hip.DitBlock.from_host(cfg, w, hip.F32)
+        try:
+            blk.set_runtime_shape(T, H, W)
+            if capture:
+                blk.set_debug({"qkv_vid": torch.empty((Lv, 3 * dim), device=device)})
+            blk.forward(rows[:Lv], rows[Lv:], e, out[:Lv], out[Lv:])
+            torch.cuda.synchronize()
+            assert blk.last_forward_merged() == (not last and not capture), (last, capture)
+        finally:
+            blk.close()

@@ -133,3 +133,26 @@ def test_unsupported_shapes(hip):
     with pytest.raises(hip.Sv2Error) as e:
         hip.inner_product_f16(x, w, y)  # out not a multiple of 256
     assert e.value.code == hip.SV2_EUNSUPPORTED
+
+
+def test_x_operand_just_under_2gib(hip):
+    """X of (2^24 - 100) rows x 64 in: 2 GiB less 12.8 KB, the largest kind of
+    operand the 32-bit buffer offsets admit, with a ragged last row tile whose
+    padded rows' offsets pass INT_MAX (formed unsigned in the kernel, and
+    returned as zeros by the buffer resource).  Rows at the start, around the
+    2^30-byte and 2^31 - 1 marks and at the end against the float64
+    product."""
+    rows, k, n = (1 << 24) - 100, 64, 256
+    print(f"[gemm] rows={rows} k={k} n={n} (X {rows * k * 2 / 2**30:.4f} GiB)", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    hip.inner_product_f16(x, w, y)
+    torch.cuda.synchronize()
+    idx = np.array(sorted({0, 1, (1 << 23) - 1, 1 << 23, rows - 257, rows - 256, rows - 2, rows - 1}))
+    got = y[torch.from_numpy(idx).cuda()].cpu().numpy()
+    ref, slack = reference64(x, w, idx)
+    assert_ulp(got, ref, slack=slack)
+    del x, y
+    torch.cuda.empty_cache()
