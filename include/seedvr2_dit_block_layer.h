@@ -41,16 +41,125 @@
  *                of the device forward.  The forward is staged through device
  *                memory (sv2_block_forward_host).
  *   set_runtime_shape / set_debug_tensors  as the reference (:609-620).
+ *
+ * The device side, in place of the reference's Vulkan path (upload_model
+ * :1271-1300, forward over VkMat :1302-1677), with sv2::DeviceMat blobs and an
+ * sv2::DeviceCompute (the HIP stream and the device allocators, the roles of
+ * VkCompute and opt.blob_vkallocator / opt.workspace_vkallocator):
+ *   upload_model the device block from the loaded weights, when
+ *                create_pipeline has not made it (a no-op otherwise).
+ *   forward      bottoms vid [L_v, dim] and txt [L_t, dim] in the compute
+ *                dtype (4-byte elements for fp32, 2-byte for fp16), emb
+ *                [6*dim] fp32, vid_shape [3] (checked for size only: the grid
+ *                is the one set_runtime_shape injected, as the reference's
+ *                Vulkan forward reads it, :1317-1324); tops from
+ *                cmd.blob_allocator in the compute dtype.  It only enqueues on
+ *                cmd.stream: no host wait, no host copy of any blob.  The
+ *                scratch comes from cmd.workspace_allocator and goes back to
+ *                it when forward returns, while the enqueued work may still
+ *                use it: the allocators must hand a freed buffer only to
+ *                work enqueued later on the same stream (a caching pool used
+ *                with one stream does).  -1 for blob counts, shapes or
+ *                element sizes that do not match or a missing runtime shape,
+ *                -100 for a failed allocation or launch.
  */
 #pragma once
 
 #include <cstdio>
+#include <memory>
 #include <vector>
 
 #include "seedvr2_hip.h"
 
+/* hipStream_t as the HIP runtime declares it, so this header needs no HIP
+ * headers. */
+struct ihipStream_t;
+typedef struct ihipStream_t* hipStream_t;
+
 namespace sv2
 {
+
+/* Device memory for DeviceMat blobs (ncnn::VkAllocator's role): fastMalloc
+ * returns device memory or NULL, fastFree takes it back. */
+class DeviceAllocator
+{
+  public:
+    virtual ~DeviceAllocator() = default;
+    virtual void* fastMalloc(size_t bytes) = 0;
+    virtual void fastFree(void* ptr) = 0;
+};
+
+/* A blob in device memory, pack 1, rows of w elements of elemsize bytes
+ * (ncnn::VkMat's role for this layer).  Copies share the buffer; the last
+ * copy to go returns it to its allocator.  borrow() wraps memory the caller
+ * owns. */
+struct DeviceMat
+{
+    int dims = 0;
+    int w = 0;
+    int h = 0;
+    size_t elemsize = 0;
+    void* data = nullptr;
+    std::shared_ptr<void> mem;
+
+    void create(int w_, size_t es, DeviceAllocator* allocator)
+    {
+        allocate(1, w_, 1, es, allocator);
+    }
+    void create(int w_, int h_, size_t es, DeviceAllocator* allocator)
+    {
+        allocate(2, w_, h_, es, allocator);
+    }
+    bool empty() const
+    {
+        return data == nullptr || size_t(w) * size_t(h) == 0;
+    }
+    void release()
+    {
+        mem.reset();
+        data = nullptr;
+        dims = w = h = 0;
+        elemsize = 0;
+    }
+    static DeviceMat borrow(void* ptr, int w_, int h_, size_t es, int dims_ = 2)
+    {
+        DeviceMat m;
+        m.dims = dims_;
+        m.w = w_;
+        m.h = h_;
+        m.elemsize = es;
+        m.data = ptr;
+        return m;
+    }
+
+  private:
+    void allocate(int d, int w_, int h_, size_t es, DeviceAllocator* allocator)
+    {
+        release();
+        dims = d;
+        w = w_;
+        h = h_;
+        elemsize = es;
+        const size_t bytes = size_t(w_ > 0 ? w_ : 0) * size_t(h_ > 0 ? h_ : 0) * es;
+        if (!bytes || !allocator)
+            return;
+        void* p = allocator->fastMalloc(bytes);
+        if (!p)
+            return;
+        mem = std::shared_ptr<void>(p, [allocator](void* q) { allocator->fastFree(q); });
+        data = p;
+    }
+};
+
+/* Where a device forward records its work (ncnn::VkCompute's role): the HIP
+ * stream (NULL: the null stream) and the allocators of the tops and of the
+ * scratch. */
+struct DeviceCompute
+{
+    hipStream_t stream = nullptr;
+    DeviceAllocator* blob_allocator = nullptr;
+    DeviceAllocator* workspace_allocator = nullptr;
+};
 
 /* The captures of SeedVR2DiTBlockDebugTensors (seedvr2_dit_block.h:20-36),
  * over the caller's Mat type; forward sizes and fills each one. */
@@ -143,6 +252,7 @@ class DiTBlockLayer : public Api::Layer
         const sv2_block_branch vid = view(branch_[0]);
         const sv2_block_branch txt = view(branch_[config_.shared_weights ? 0 : 1]);
         const int dtype = opt.use_fp16_arithmetic ? SV2_F16 : SV2_F32;
+        compute_dtype_ = dtype;
         const int rc = sv2_block_create(&config_, &vid, &txt, static_cast<const float*>(freqs_.data), 0, dtype, &block_);
         if (rc != SV2_OK)
         {
@@ -216,6 +326,67 @@ class DiTBlockLayer : public Api::Layer
             return -100;
         }
         return 0;
+    }
+
+    /* The device block from the loaded weights, when create_pipeline has not
+     * made it (SeedVR2DiTBlock::upload_model, seedvr2_dit_block.cpp:1271). */
+    int upload_model(DeviceCompute&, const Option& opt)
+    {
+        return block_ ? 0 : create_pipeline(opt);
+    }
+
+    /* The block forward over device blobs: enqueued on cmd.stream only
+     * (SeedVR2DiTBlock::forward over VkMat, seedvr2_dit_block.cpp:1302-1324
+     * for the checks). */
+    int forward(const std::vector<DeviceMat>& bottom_blobs, std::vector<DeviceMat>& top_blobs, DeviceCompute& cmd,
+                const Option&) const
+    {
+        if (bottom_blobs.size() != 4 || top_blobs.size() != 2)
+            return -1;
+        const DeviceMat& vid = bottom_blobs[0];
+        const DeviceMat& txt = bottom_blobs[1];
+        const DeviceMat& emb = bottom_blobs[2];
+        const DeviceMat& shape = bottom_blobs[3];
+        const int D = config_.dim;
+        if (vid.dims != 2 || vid.w != D || txt.dims != 2 || txt.w != D || emb.w != 6 * D || shape.w != 3)
+            return -1;
+        if (!block_ || !shape_valid_ || int64_t(frames_) * height_ * width_ != vid.h)
+            return -1;
+        const size_t es = dtype_bytes();
+        if (vid.elemsize != es || (txt.h > 0 && txt.elemsize != es) || emb.elemsize != 4 || vid.empty() ||
+            emb.empty() || (txt.h > 0 && txt.empty()))
+            return -1;
+        const int Lv = vid.h, Lt = txt.h;
+        DeviceMat& vid_out = top_blobs[0];
+        DeviceMat& txt_out = top_blobs[1];
+        vid_out.create(D, Lv, es, cmd.blob_allocator);
+        txt_out.create(D, Lt, es, cmd.blob_allocator);
+        if (vid_out.empty() || (Lt > 0 && txt_out.empty()))
+            return -100;
+        const int64_t need = sv2_block_workspace_size(block_, Lt);
+        if (need < 0)
+            return -100;
+        DeviceMat ws;
+        ws.create(static_cast<int>(need > 0 ? need : 1), size_t(1u), cmd.workspace_allocator);
+        if (ws.empty())
+            return -100;
+        const int rc = sv2_block_forward(block_, vid.data, Lt > 0 ? txt.data : nullptr, Lt,
+                                         static_cast<const float*>(emb.data), vid_out.data,
+                                         Lt > 0 ? txt_out.data : nullptr, ws.data, size_t(need),
+                                         static_cast<void*>(cmd.stream));
+        if (rc != SV2_OK)
+        {
+            std::fprintf(stderr, "SeedVR2DiTBlock[%d]: %s\n", config_.block_index, sv2_last_error());
+            return -100;
+        }
+        return 0;
+    }
+
+    /* Bytes per element of the device blobs: 2 in the fp16 compute mode, 4
+     * in fp32 (0 before create_pipeline). */
+    size_t dtype_bytes() const
+    {
+        return block_ ? (compute_dtype_ == SV2_F16 ? 2u : 4u) : 0u;
     }
 
     /* The patched grid of the next device forward (the ncnn CPU forward reads
@@ -310,6 +481,7 @@ class DiTBlockLayer : public Api::Layer
     Branch branch_[2];
     Mat freqs_;
     sv2_block* block_ = nullptr;
+    int compute_dtype_ = SV2_F32;
     int frames_ = 0, height_ = 0, width_ = 0;
     bool shape_valid_ = false;
     DebugTensors* debug_ = nullptr;

@@ -12,16 +12,31 @@
 //   block_runner --load-only model.param model.bin
 //       parses and loads the block without a device and prints its
 //       parameters and the bytes of the .bin left unread.
+//   block_runner --device-chain N b0.param b0.bin ... vid.f32 vid_rows
+//                txt.f32 txt_rows emb.f32 T H W vid_out.f32 txt_out.f32
+//       N blocks chained on device blobs (sv2::DeviceMat) through the
+//       adapter's upload_model and device forward, as the reference DiT
+//       drives its blocks on VkMat (src/model/dit.cpp:545-581): the inputs
+//       are uploaded once, each block's tops are the next block's bottoms,
+//       every forward enqueues on one HIP stream, and the host waits and
+//       downloads once, after the last block.  Blobs come from a caching
+//       device pool (freed buffers reused by later allocations on the same
+//       stream).
 //
 // Exit codes as the reference runner: 2 usage, 3 inputs, 4 model load,
 // 6 inference, 7 outputs, 8 captures.
+#include <hip/hip_runtime_api.h>
+
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
+#include <map>
+#include <memory>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "layer_types.h"
 #include "seedvr2_dit_block_layer.h"
@@ -65,6 +80,219 @@ bool write_matrix(const std::string& path, const host::Mat& m)
     return bool(out);
 }
 
+// A caching pool of device buffers (a blob allocator in ncnn's sense): a
+// freed buffer goes back to the pool and serves a later request of at most
+// its size.  With one stream, stream order makes the reuse safe: work that
+// reads a freed buffer was enqueued before the work that writes its reuse.
+class DevicePool : public sv2::DeviceAllocator
+{
+  public:
+    ~DevicePool() override
+    {
+        for (auto& kv : size_)
+            (void)hipFree(kv.first);
+    }
+    void* fastMalloc(size_t bytes) override
+    {
+        auto it = free_.lower_bound(bytes);
+        if (it != free_.end() && it->first <= 2 * bytes + 4096)
+        {
+            void* p = it->second;
+            free_.erase(it);
+            return p;
+        }
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess)
+            return nullptr;
+        size_[p] = bytes;
+        return p;
+    }
+    void fastFree(void* ptr) override
+    {
+        if (ptr)
+            free_.emplace(size_[ptr], ptr);
+    }
+
+  private:
+    std::map<void*, size_t> size_;
+    std::multimap<size_t, void*> free_;
+};
+
+uint16_t float_to_half(float f)
+{
+    // round to nearest even, as the library's fp32 -> fp16 conversions
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int exp = int((x >> 23) & 0xffu) - 127 + 15;
+    uint32_t mant = x & 0x7fffffu;
+    if (((x >> 23) & 0xffu) == 0xffu)
+        return uint16_t(sign | 0x7c00u | (mant ? 0x200u : 0u));
+    if (exp >= 31)
+        return uint16_t(sign | 0x7c00u);
+    if (exp <= 0)
+    {
+        if (exp < -10)
+            return uint16_t(sign);
+        mant |= 0x800000u;
+        const int shift = 14 - exp;
+        uint32_t h = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1u)))
+            h++;
+        return uint16_t(sign | h);
+    }
+    uint32_t h = (uint32_t(exp) << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u)))
+        h++;
+    return uint16_t(sign | h);
+}
+
+SeedVR2DiTBlock* find_block(host::Net& net);
+
+// Host fp32 values -> a device blob in the compute dtype (elements of es = 2
+// or 4 bytes), [h][w] (dims 2) or [w] (dims 1).
+bool upload(const host::Mat& m, size_t es, DevicePool& pool, sv2::DeviceMat* out)
+{
+    if (m.dims == 1)
+        out->create(m.w, es, &pool);
+    else
+        out->create(m.w, m.h, es, &pool);
+    const size_t n = size_t(m.w) * size_t(m.h);
+    if (n == 0)
+        return true;
+    if (out->empty())
+        return false;
+    const float* src = static_cast<const float*>(m.data);
+    if (es == 4)
+        return hipMemcpy(out->data, src, n * 4, hipMemcpyHostToDevice) == hipSuccess;
+    std::vector<uint16_t> half(n);
+    for (size_t i = 0; i < n; i++)
+        half[i] = float_to_half(src[i]);
+    return hipMemcpy(out->data, half.data(), n * 2, hipMemcpyHostToDevice) == hipSuccess;
+}
+
+// A device blob in the compute dtype -> host fp32 rows.
+bool download(const sv2::DeviceMat& d, host::Mat* out)
+{
+    out->create(d.w, d.h, size_t(4u));
+    const size_t n = size_t(d.w) * size_t(d.h);
+    if (n == 0)
+        return true;
+    if (out->empty() || d.empty())
+        return false;
+    float* dst = static_cast<float*>(out->data);
+    if (d.elemsize == 4)
+        return hipMemcpy(dst, d.data, n * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    std::vector<uint16_t> half(n);
+    if (hipMemcpy(half.data(), d.data, n * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return false;
+    for (size_t i = 0; i < n; i++)
+        dst[i] = host::half_to_float(half[i]);
+    return true;
+}
+
+// --device-chain: argv[2] = N, then N (param, bin) pairs, then the inputs and
+// outputs of the single-block form.
+int device_chain(int argc, char** argv)
+{
+    const int n = argc > 2 ? std::atoi(argv[2]) : 0;
+    if (n < 1 || argc != 3 + 2 * n + 10)
+    {
+        std::fprintf(stderr, "usage: %s --device-chain N b0.param b0.bin ... vid.f32 vid_rows txt.f32 txt_rows "
+                             "emb.f32 T H W vid_out.f32 txt_out.f32\n", argv[0]);
+        return 2;
+    }
+    char** a = argv + 3 + 2 * n;
+    const int vid_rows = std::atoi(a[1]);
+    const int txt_rows = std::atoi(a[3]);
+    const int frames = std::atoi(a[5]), height = std::atoi(a[6]), width = std::atoi(a[7]);
+    const char* fp16 = std::getenv("SEEDVR2_FP16");
+    std::vector<std::unique_ptr<host::Net>> nets;
+    std::vector<SeedVR2DiTBlock*> layers;
+    DevicePool pool;
+    hipStream_t stream = nullptr;
+    if (hipStreamCreate(&stream) != hipSuccess)
+        return 6;
+    sv2::DeviceCompute cmd;
+    cmd.stream = stream;
+    cmd.blob_allocator = &pool;
+    cmd.workspace_allocator = &pool;
+    for (int i = 0; i < n; i++)
+    {
+        auto net = std::make_unique<host::Net>();
+        net->opt.use_fp16_arithmetic = fp16 && std::string(fp16) == "1";
+        net->register_custom_layer("SeedVR2DiTBlock", SeedVR2DiTBlock_layer_creator);
+        if (net->load_param(argv[3 + 2 * i]) != 0 || net->load_model(argv[4 + 2 * i]) != 0)
+        {
+            std::fprintf(stderr, "failed to load block %d\n", i);
+            return 4;
+        }
+        SeedVR2DiTBlock* layer = find_block(*net);
+        if (!layer || layer->upload_model(cmd, net->opt) != 0)
+            return 4;
+        layers.push_back(layer);
+        nets.push_back(std::move(net));
+    }
+    const int dim = layers[0]->config().dim;
+    const size_t es = layers[0]->dtype_bytes();
+    host::Mat vid, txt, emb;
+    if (!read_matrix(a[0], vid_rows, dim, vid) || !read_matrix(a[2], txt_rows, dim, txt) ||
+        !read_matrix(a[4], 1, 6 * dim, emb))
+    {
+        std::fprintf(stderr, "failed to read input matrices\n");
+        return 3;
+    }
+    emb.dims = 1; // a [6*dim] vector, as the emb blob
+    host::Mat shape(3, size_t(4u));
+    static_cast<int*>(shape.data)[0] = frames;
+    static_cast<int*>(shape.data)[1] = height;
+    static_cast<int*>(shape.data)[2] = width;
+    std::vector<sv2::DeviceMat> bottoms(4);
+    if (!upload(vid, es, pool, &bottoms[0]) || !upload(txt, es, pool, &bottoms[1]) ||
+        !upload(emb, 4, pool, &bottoms[2]) || !upload(shape, 4, pool, &bottoms[3]))
+    {
+        std::fprintf(stderr, "failed to upload the inputs\n");
+        return 3;
+    }
+    const auto start = std::chrono::steady_clock::now();
+    for (int i = 0; i < n; i++)
+    {
+        layers[i]->set_runtime_shape(frames, height, width);
+        std::vector<sv2::DeviceMat> tops(2);
+        const int rc = layers[i]->forward(bottoms, tops, cmd, nets[i]->opt);
+        if (rc != 0)
+        {
+            std::fprintf(stderr, "block %d inference failed (%d)\n", i, rc);
+            return 6;
+        }
+        // the next block reads these tops; the previous bottoms go back to the pool
+        bottoms[0] = tops[0];
+        bottoms[1] = tops[1];
+    }
+    const double enqueue_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
+    if (hipStreamSynchronize(stream) != hipSuccess)
+    {
+        std::fprintf(stderr, "device chain failed on the stream\n");
+        return 6;
+    }
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
+    std::printf("device_chain blocks=%d enqueue_ms=%.3f total_ms=%.3f\n", n, enqueue_ms, ms);
+    host::Mat vo, to;
+    if (!download(bottoms[0], &vo) || !download(bottoms[1], &to) || !write_matrix(a[8], vo) ||
+        !write_matrix(a[9], to))
+    {
+        std::fprintf(stderr, "failed to write block outputs\n");
+        return 7;
+    }
+    bottoms.clear();
+    (void)hipStreamDestroy(stream);
+    return 0;
+}
+
 SeedVR2DiTBlock* find_block(host::Net& net)
 {
     for (host::Layer* l : net.mutable_layers())
@@ -76,6 +304,8 @@ SeedVR2DiTBlock* find_block(host::Net& net)
 
 int main(int argc, char** argv)
 {
+    if (argc > 1 && std::string(argv[1]) == "--device-chain")
+        return device_chain(argc, argv);
     if (argc == 4 && std::string(argv[1]) == "--load-only")
     {
         host::Net net;

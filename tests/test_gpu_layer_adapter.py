@@ -130,3 +130,79 @@ def test_runner_equals_device_entry_points(hip, orc, device, tmp_path, case, dty
                 continue
             d = np.abs(a.astype(np.float64) - b)
             assert d.max() <= 2e-3 and d.mean() <= 2e-4, (d.max(), d.mean())
+
+
+CHAINS = [
+    # blocks as (shared, last, shifted): an unshifted non-shared block, a
+    # shifted shared one, then (in the 3-block chain) a shared last layer
+    ("two", [(False, False, False), (True, False, True)], 7),
+    ("three_last", [(False, False, True), (True, False, False), (True, True, True)], 5),
+    ("no_text", [(False, False, False), (False, False, True)], 0),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("chain", CHAINS, ids=[c[0] for c in CHAINS])
+def test_device_chain_equals_device_entry_points(hip, device, tmp_path, chain, dtype):
+    """The adapter's device forward (sv2::DiTBlockLayer over sv2::DeviceMat
+    blobs, enqueue only) chained as the reference DiT chains its blocks on
+    VkMat (src/model/dit.cpp:545-581): tests/cxx/block_runner --device-chain
+    uploads the inputs once, feeds each block's tops to the next block and
+    downloads once.  Against the same blocks chained through sv2_block_forward
+    in this process: bit for bit in fp32; within the reference's block gate
+    in fp16 (the runner maps the ROCm hipBLASLt, this process torch's copy)."""
+    name, flags, L = chain
+    assert RUNNER.exists(), "tests/cxx/_build/block_runner is not built (build() compiles it)"
+    dim, heads, hidden, (T, H, W) = 256, 2, 512, (3, 8, 12)
+    print(f"[device chain] {name} {dtype} blocks={len(flags)} L={L}", flush=True)
+    rng = np.random.default_rng(100 + len(flags) + L)
+    files = []
+    for i, (shared, last, shifted) in enumerate(flags):
+        w = nf.random_weights(rng, dim, hidden, shared=shared)
+        param, binf = tmp_path / f"b{i}.param", tmp_path / f"b{i}.bin"
+        nf.write_param(param, index=i, shared=shared, last=last, shifted=shifted, dim=dim, heads=heads,
+                       mlp_hidden=hidden)
+        nf.write_bin(binf, w, shared=shared, storage="fp16")
+        files += [param, binf]
+    vid = rng.standard_normal((T * H * W, dim), dtype=np.float32)
+    txt = rng.standard_normal((L, dim), dtype=np.float32)
+    emb = rng.standard_normal(6 * dim, dtype=np.float32)
+    io = {k: tmp_path / f"{k}.f32" for k in ("vid", "txt", "emb")}
+    for k, a in (("vid", vid), ("txt", txt), ("emb", emb)):
+        np.ascontiguousarray(a, "<f4").tofile(io[k])
+    env = dict(os.environ, SEEDVR2_FP16="1" if dtype == "f16" else "0")
+    cmd = [RUNNER, "--device-chain", len(flags), *files, io["vid"], T * H * W, io["txt"], L, io["emb"], T, H, W,
+           tmp_path / "vo.f32", tmp_path / "to.f32"]
+    r = subprocess.run([str(c) for c in cmd], capture_output=True, text=True, timeout=120, env=env)
+    print(r.stdout.strip(), r.stderr.strip(), flush=True)
+    assert r.returncode == 0, r.stderr
+    rv, rt = read_matrix(tmp_path / "vo.f32"), read_matrix(tmp_path / "to.f32")
+    assert rv.shape == (T * H * W, dim) and rt.shape == (L, dim)
+
+    code = hip.F32 if dtype == "f32" else hip.F16
+    td = torch.float32 if dtype == "f32" else torch.float16
+    v = torch.from_numpy(vid).to(device=device, dtype=td)
+    t = torch.from_numpy(txt).to(device=device, dtype=td)
+    e = torch.from_numpy(emb).to(device)
+    for i in range(len(flags)):
+        blk = hip.DitBlock.load(files[2 * i], files[2 * i + 1], code)
+        try:
+            blk.set_runtime_shape(T, H, W)
+            vo, to = torch.full_like(v, float("nan")), torch.full_like(t, float("nan"))
+            blk.forward(v, t if L else None, e, vo, to if L else None)
+            torch.cuda.synchronize()
+        finally:
+            blk.close()
+        v, t = vo, to
+    dv, dt = v.float().cpu().numpy(), t.float().cpu().numpy()
+    for k, a, b in (("vid_out", rv, dv), ("txt_out", rt, dt)):
+        differing = int((a.view(np.uint32) != b.view(np.uint32)).sum())
+        print(f"  {k}: {differing} of {a.size} elements differ", flush=True)
+        if dtype == "f32":
+            assert differing == 0, k
+        elif a.size:
+            d = a.astype(np.float64) - b
+            rms = max(float(np.sqrt(np.mean(b.astype(np.float64) ** 2))), 1e-12)
+            cos = float(np.sum(a * b.astype(np.float64)) /
+                        max(np.sqrt(np.sum(a.astype(np.float64) ** 2) * np.sum(b.astype(np.float64) ** 2)), 1e-30))
+            assert np.isfinite(a).all() and float(np.sqrt(np.mean(d * d))) / rms <= 2e-3 and cos >= 0.99999, k
