@@ -8,7 +8,8 @@ Gates:
     fp32 upcast; in fp16 mode NRMSE <= 2e-3;
   * the whole DiT (32 blocks): the reference's full-model criteria, NRMSE <=
     0.02 and cosine >= 0.9998 (tools/test_seedvr2_dit_ncnn.py:249-250), in
-    both compute modes, with max/mean-abs reported.
+    both compute modes; in the fp32 parity mode also max-abs <= 2e-3 and
+    mean-abs <= 2e-4.
 The heads run at the real widths (dim 2560, 33 latent channels, 5120 text
 channels, 256 sinusoid, 16 output channels) on a small grid; the DiT runs at
 width 256 (2 heads, MLP 512) with the exporter's 32-block layout (shared
@@ -228,7 +229,14 @@ def test_dit_32_blocks(hip, orc, device, dtype):
     finally:
         dit.close()
     r = oracle_dit(orc, wi, blocks_w, wo, latent, text, 1000.0)
-    gate_full(metrics(g, r), f"dit {dtype}")
+    rep = metrics(g, r)
+    gate_full(rep, f"dit {dtype}")
+    if code == hip.F32:
+        # the parity mode computes each block's arithmetic as the oracle does
+        # (NRMSE measured ~1e-6 over the 32 blocks): held to the element-wise
+        # gate of one block, so a regression far below the full-model
+        # criterion still fails
+        assert rep["max_abs"] <= 2e-3 and rep["mean_abs"] <= 2e-4, rep
 
 
 def test_dit_load_model_dir(hip, orc, device, tmp_path):

@@ -128,10 +128,11 @@ def test_exact_reference_adaptive_windows(hip, orc, device, shifted):
                seed=4 + shifted)
 
 
-def test_exact_720p_sampled_windows(hip, orc, device):
-    n = len(orc.make_windows(6, 45, 80, True, 2, 9, 16))
-    exact_case(hip, orc, device, T=6, H=45, W=80, Lt=L_TXT, heads=20, shifted=True, wt=2, wh=9, ww=16,
-               seed=10, out_dtype="f16", video_windows=sorted({0, n // 2, n - 1}))
+@pytest.mark.parametrize("shifted", [False, True], ids=["unshifted", "shifted"])
+def test_exact_720p_all_windows(hip, orc, device, shifted):
+    # every window of both 720p plans, video and text outputs
+    exact_case(hip, orc, device, T=6, H=45, W=80, Lt=L_TXT, heads=20, shifted=shifted, wt=2, wh=9, ww=16,
+               seed=10 + shifted, out_dtype="f16")
 
 
 @pytest.mark.parametrize("case", [
