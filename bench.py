@@ -146,6 +146,157 @@ def cpu_baseline(target_s: float = 15.0):
     }
 
 
+def mapped_libraries(fragment: str) -> list:
+    """Paths of the shared objects mapped into this process whose name holds
+    `fragment` (which hipBLASLt copy the fp16 InnerProducts ran on)."""
+    out = set()
+    try:
+        for line in Path("/proc/self/maps").read_text().splitlines():
+            parts = line.split()
+            if len(parts) >= 6 and fragment in parts[-1]:
+                out.add(parts[-1])
+    except OSError:
+        pass
+    return sorted(out)
+
+
+def _median_ms(fn, runs=3):
+    fn()  # warmup
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return float(np.median(ts))
+
+
+def _gpu_ms(fn, reps=20):
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def _row(name, variant, ms, flops, nbytes, cpu_ms, cores, err, passed):
+    t = ms * 1e-3
+    return {"config": name, "variant": variant, "gpu_ms": round(ms, 4), "tflops": round(flops / t / 1e12, 2),
+            "mfma_pct": round(100 * flops / t / 1e12 / PEAK_FP16_TFLOPS, 2),
+            "hbm_gbs": round(nbytes / t / 1e9, 1), "hbm_pct": round(100 * nbytes / t / 1e9 / PEAK_HBM_GBS, 2),
+            "roofline_pct": round(100 * max(flops / (PEAK_FP16_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) / t, 2),
+            "cpu_ms": None if cpu_ms is None else round(cpu_ms, 1), "cpu_cores": cores, **err, "pass": passed}
+
+
+def config_table(dev, with_cpu: bool):
+    """One row per configuration of the metric's config list that fits a GPU
+    and the CPU beside it: the single windowed MM-attention layer at the
+    480x256x5 grid 2x16x30 (config 1: fp32, no RoPE, no QK-norm, 2x8x10
+    unshifted windows; config 2: fp16, QK-RMSNorm + RoPE, unshifted and
+    shifted) and one DiT block at that grid (config 4: hidden 2560, 20 heads,
+    MLP 6912, fp16 weights N(0, 0.02^2), fp16 inputs N(0, 1), 58 text tokens).
+    GPU ms: mean over 20 launches after 3 warmups (HIP events); CPU ms: the
+    oracle's median of 3 after a warmup, on the same inputs; errors of the
+    GPU outputs against the oracle's (the attention's gates: max-abs <= 2e-3
+    / mean-abs <= 2e-4 but for one-ulp bf16 flips; the block's: NRMSE <=
+    2e-3).  Config 3 is the line's own workload; config 5 the dit_step."""
+    import torch
+    import oracle
+    import sv2hip
+    from parity import cast_like, reference_freqs, report
+    import ncnn_files as nf
+    oracle.load()
+    host = host_cpu()
+    threads = host["nproc"]
+    if host["omp_num_threads"]:
+        threads = min(threads, int(host["omp_num_threads"]))
+    Tg, Hg, Wg, D = 2, 16, 30, HEADS * HD
+    Lv = Tg * Hg * Wg
+    freqs = reference_freqs()
+    rows = []
+    tdt = {"f32": torch.float32, "f16": torch.float16}
+    for name, in_dt, norm, rope, shifted in (("1", "f32", False, sv2hip.ROPE_NONE, False),
+                                             ("2", "f16", True, sv2hip.ROPE_REFERENCE, False),
+                                             ("2", "f16", True, sv2hip.ROPE_REFERENCE, True)):
+        rng = np.random.default_rng(31 + shifted)
+        vid = cast_like(rng.standard_normal((Lv, 3 * D), dtype=np.float32), in_dt)
+        txt = cast_like(rng.standard_normal((L_TXT, 3 * D), dtype=np.float32), in_dt)
+        gam = list(rng.uniform(0.5, 1.5, (4, 128)).astype(np.float32)) if norm else None
+        wins = sv2hip.window_plan(sv2hip.rule(Tg, Hg, Wg, shifted, 2, 8, 10))
+        sizes = [(w[1] - w[0]) * (w[3] - w[2]) * (w[5] - w[4]) for w in wins]
+        flops = sum(4.0 * (v + L_TXT) ** 2 * HD * HEADS for v in sizes)
+        es = 4 if in_dt == "f32" else 2
+        nbytes = (Lv + L_TXT) * HEADS * HD * es * 4
+        attn = sv2hip.WindowAttention(sv2hip.rule(Tg, Hg, Wg, shifted, 2, 8, 10), HEADS, L_TXT, qk_norm=norm,
+                                      rope_mode=rope, freqs=freqs, device=dev)
+        tv = torch.from_numpy(vid).to(dev, tdt[in_dt])
+        tt = torch.from_numpy(txt).to(dev, tdt[in_dt])
+        tg = None if gam is None else [torch.from_numpy(g).to(dev) for g in gam]
+        ov = torch.empty((Lv, D), dtype=tdt[in_dt], device=dev)
+        ot = torch.empty((L_TXT, D), dtype=tdt[in_dt], device=dev)
+        ms = _gpu_ms(lambda: attn(tv, tt, tg, ov, ot))
+        ref = {}
+
+        def run_cpu():
+            ref["v"], ref["t"] = oracle.window_attention(vid, txt, Tg, Hg, Wg, heads=HEADS, qk_norm=norm,
+                                                         rope_mode=rope, freqs=freqs, gammas=gam, shifted=shifted,
+                                                         wt=2, wh=8, ww=10, threads=threads)
+        cpu_ms = _median_ms(run_cpu) if with_cpu else None
+        if not with_cpu:
+            run_cpu()
+        rep = report(ov.float().cpu().numpy(), cast_like(ref["v"], in_dt))
+        err = {"max_abs": rep["max_abs"], "mean_abs": rep["mean_abs"], "flips": rep["flips"]}
+        passed = bool(rep["finite"] and rep["over_tol_not_flip"] == 0 and rep["mean_abs"] <= 2e-4)
+        rows.append(_row(name, f"2x8x10 {'shifted' if shifted else 'unshifted'}, "
+                               f"{'no RoPE / no QK-norm' if not norm else 'QK-RMSNorm + reference RoPE'}, {in_dt}",
+                         ms, flops, nbytes, cpu_ms, threads, err, passed))
+
+    # config 4: one block, fp16 compute, against the oracle's fp32 block
+    rng = np.random.default_rng(41)
+    w = nf.random_weights(rng, D, DIT_FFN, shared=False)
+    vid = rng.standard_normal((Lv, D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    txt = rng.standard_normal((L_TXT, D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    emb = rng.standard_normal(6 * D, dtype=np.float32)
+    blk = sv2hip.DitBlock.from_host(sv2hip.block_config(dim=D, heads=HEADS, mlp_hidden=DIT_FFN, window_t=2,
+                                                        window_h=8, window_w=10), w, sv2hip.F16)
+    blk.set_runtime_shape(Tg, Hg, Wg)
+    tv = torch.from_numpy(vid).to(dev, torch.float16)
+    tt = torch.from_numpy(txt).to(dev, torch.float16)
+    te = torch.from_numpy(emb).to(dev)
+    ov, ot = torch.empty_like(tv), torch.empty_like(tt)
+    ws = torch.empty(blk.workspace_size(L_TXT), dtype=torch.uint8, device=dev)
+    ms = _gpu_ms(lambda: blk.forward(tv, tt, te, ov, ot, workspace=ws))
+    gv = ov.float().cpu().numpy()
+    blk.close()
+    ref = {}
+
+    def run_block():
+        ref["v"], ref["t"] = oracle.block_forward(w, vid, txt, emb, Tg, Hg, Wg, dim=D, heads=HEADS,
+                                                  mlp_hidden=DIT_FFN, shared=False, shifted=False, wt=2, wh=8, ww=10,
+                                                  threads=threads)
+    cpu_ms = _median_ms(run_block) if with_cpu else None
+    if not with_cpu:
+        run_block()
+    d = gv.astype(np.float64) - ref["v"]
+    rms = max(float(np.sqrt(np.mean(ref["v"].astype(np.float64) ** 2))), 1e-12)
+    nrmse = float(np.sqrt(np.mean(d * d))) / rms
+    rows_tok = Lv + L_TXT
+    gemm = 2.0 * rows_tok * D * (3 * D + D + 3 * DIT_FFN)
+    attn_f = sum(4.0 * (v + L_TXT) ** 2 * HD * HEADS for v in
+                 [(x[1] - x[0]) * (x[3] - x[2]) * (x[5] - x[4])
+                  for x in sv2hip.window_plan(sv2hip.rule(Tg, Hg, Wg, False, 2, 8, 10))])
+    wbytes = 2 * 2 * (3 * D * D + D * D + 3 * D * DIT_FFN)  # two branches of fp16 matrices
+    err = {"max_abs": float(np.abs(d).max()), "mean_abs": float(np.abs(d).mean()), "nrmse": nrmse}
+    rows.append(_row("4", "one block 960+58 tokens, 2x8x10 unshifted, fp16 (InnerProducts on hipBLASLt)",
+                     ms, gemm + attn_f, wbytes, cpu_ms, threads, err, bool(np.isfinite(gv).all() and nrmse <= 2e-3)))
+    return rows
+
+
 DIT_DIM, DIT_FFN, DIT_BLOCKS, LATENT_C, TEXT_C, OUT_C = 2560, 6912, 32, 33, 5120, 16
 
 
@@ -331,6 +482,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--no-table", action="store_true",
+                    help="skip the per-configuration rows (configs 1, 2 and 4 on the GPU and the CPU oracle)")
     ap.add_argument("--dit-steps", type=int, default=3, help="timed DiT forwards (0 skips the DiT leg)")
     ap.add_argument("--dit-only", action="store_true",
                     help="run only the DiT leg and print its figures (for profiling the DiT step)")
@@ -461,6 +614,9 @@ def main():
         result["config"]["dit_step_ms"] = ds["ms"]
         result["config"]["dit_step"] = ds
     result["config"]["sampler_step"] = sampler_bench(dev)
+    if not args.no_table:
+        result["config"]["configs"] = config_table(dev, not args.no_cpu)
+    result["config"]["hipblaslt_mapped"] = mapped_libraries("libhipblaslt")
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))
