@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -158,6 +159,25 @@ def mapped_libraries(fragment: str) -> list:
     except OSError:
         pass
     return sorted(out)
+
+
+def dit_step_cxx(steps: int) -> dict:
+    """The same DiT forward driven from C++ through the C ABI alone
+    (tests/cxx/dit_step, a child process without torch): the time a C++
+    integration sees, on the libhipblaslt it maps itself (ROCm's), against
+    dit_step's, whose process maps the copy bundled with torch."""
+    exe = Path(__file__).resolve().parent / "tests" / "cxx" / "_build" / "dit_step"
+    if not exe.exists():
+        return {"error": "tests/cxx/_build/dit_step is not built (build() compiles it)"}
+    try:
+        proc = subprocess.run([str(exe), "--steps", str(steps), "--warmup", "1"], capture_output=True, text=True,
+                              timeout=600)
+    except subprocess.TimeoutExpired:
+        return {"error": "dit_step timed out"}
+    lines = [ln for ln in proc.stdout.splitlines() if ln.startswith("{")]
+    if proc.returncode != 0 or not lines:
+        return {"error": f"dit_step exited {proc.returncode}: {proc.stderr.strip()[-400:]}"}
+    return json.loads(lines[-1])
 
 
 def _median_ms(fn, runs=3):
@@ -613,6 +633,7 @@ def main():
         ds = dit_bench(dev, args.dit_steps, 1)
         result["config"]["dit_step_ms"] = ds["ms"]
         result["config"]["dit_step"] = ds
+        result["config"]["dit_step_cxx"] = dit_step_cxx(args.dit_steps)
     result["config"]["sampler_step"] = sampler_bench(dev)
     if not args.no_table:
         result["config"]["configs"] = config_table(dev, not args.no_cpu)

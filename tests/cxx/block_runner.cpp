@@ -38,6 +38,7 @@
 #include <utility>
 #include <vector>
 
+#include "host_half.h"
 #include "layer_types.h"
 #include "seedvr2_dit_block_layer.h"
 
@@ -118,38 +119,6 @@ class DevicePool : public sv2::DeviceAllocator
     std::multimap<size_t, void*> free_;
 };
 
-uint16_t float_to_half(float f)
-{
-    // round to nearest even, as the library's fp32 -> fp16 conversions
-    uint32_t x;
-    std::memcpy(&x, &f, 4);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    const int exp = int((x >> 23) & 0xffu) - 127 + 15;
-    uint32_t mant = x & 0x7fffffu;
-    if (((x >> 23) & 0xffu) == 0xffu)
-        return uint16_t(sign | 0x7c00u | (mant ? 0x200u : 0u));
-    if (exp >= 31)
-        return uint16_t(sign | 0x7c00u);
-    if (exp <= 0)
-    {
-        if (exp < -10)
-            return uint16_t(sign);
-        mant |= 0x800000u;
-        const int shift = 14 - exp;
-        uint32_t h = mant >> shift;
-        const uint32_t rem = mant & ((1u << shift) - 1u);
-        const uint32_t half = 1u << (shift - 1);
-        if (rem > half || (rem == half && (h & 1u)))
-            h++;
-        return uint16_t(sign | h);
-    }
-    uint32_t h = (uint32_t(exp) << 10) | (mant >> 13);
-    const uint32_t rem = mant & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u)))
-        h++;
-    return uint16_t(sign | h);
-}
-
 SeedVR2DiTBlock* find_block(host::Net& net);
 
 // Host fp32 values -> a device blob in the compute dtype (elements of es = 2
@@ -170,7 +139,7 @@ bool upload(const host::Mat& m, size_t es, DevicePool& pool, sv2::DeviceMat* out
         return hipMemcpy(out->data, src, n * 4, hipMemcpyHostToDevice) == hipSuccess;
     std::vector<uint16_t> half(n);
     for (size_t i = 0; i < n; i++)
-        half[i] = float_to_half(src[i]);
+        half[i] = host_half::from_float(src[i]);
     return hipMemcpy(out->data, half.data(), n * 2, hipMemcpyHostToDevice) == hipSuccess;
 }
 
