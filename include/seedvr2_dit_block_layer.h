@@ -366,8 +366,14 @@ class DiTBlockLayer : public Api::Layer
         const int64_t need = sv2_block_workspace_size(block_, Lt);
         if (need < 0)
             return -100;
+        // rows of 1 MiB: a workspace past 2 GiB (large grids) keeps its byte
+        // count out of the blob's int extents
+        const int64_t row = int64_t(1) << 20;
+        const int64_t rows = need > 0 ? (need + row - 1) / row : 1;
+        if (rows > int64_t(0x7fffffff))
+            return -100;
         DeviceMat ws;
-        ws.create(static_cast<int>(need > 0 ? need : 1), size_t(1u), cmd.workspace_allocator);
+        ws.create(static_cast<int>(row), static_cast<int>(rows), size_t(1u), cmd.workspace_allocator);
         if (ws.empty())
             return -100;
         const int rc = sv2_block_forward(block_, vid.data, Lt > 0 ? txt.data : nullptr, Lt,
