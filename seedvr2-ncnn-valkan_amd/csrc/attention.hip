@@ -262,6 +262,7 @@ struct LdsLayout
     int rows;    // int2 [vmax]: global video row, packed local (t | y << 10 | x << 20)
     int rope;    // float2 [rope_rows][24]: cos/sin rows t..., y..., x... of the window
     int gamma;   // float [2][128]: q, k gammas of the video branch
+    int krope;   // int2 [16 chunks][4 pairs]: a key lane's RoPE table offset and position shift
     int total;
 };
 
@@ -847,6 +848,58 @@ __device__ inline KeyRope key_rope(const RopeBase& rb, int d0)
     return k;
 }
 
+// The window's KeyRope of every key chunk, staged once so the tile loop reads
+// a lane's four (table offset, position shift) pairs with two LDS loads: the
+// per-pair axis selection, recomputed each tile, costs divergent branches.
+// Threads 0-63 write one pair each (chunk = tid / 4, pair tid % 4); the
+// caller synchronises.
+template <int RM>
+__device__ inline void stage_key_rope(const AttnParams& p, const WindowBox& box, char* smem, int tid)
+{
+    if constexpr (RM != SV2_ROPE_NONE)
+    {
+        if (tid < 64)
+        {
+            const KeyRope k = key_rope<RM>(rope_base(box), 8 * (tid >> 2));
+            const int q = tid & 3;
+            const int off = q == 0 ? k.off[0] : (q == 1 ? k.off[1] : (q == 2 ? k.off[2] : k.off[3]));
+            const int shift = q == 0 ? k.shift[0] : (q == 1 ? k.shift[1] : (q == 2 ? k.shift[2] : k.shift[3]));
+            reinterpret_cast<int2*>(smem + p.lds.krope)[tid] = make_int2(off, shift);
+        }
+    }
+}
+
+// A key lane's KeyRope from the staged table (stage_key_rope).
+template <int RM>
+__device__ inline KeyRope staged_key_rope(const AttnParams& p, const char* smem, int chunk)
+{
+    KeyRope k;
+    if constexpr (RM != SV2_ROPE_NONE)
+    {
+        const int4* t = reinterpret_cast<const int4*>(smem + p.lds.krope) + 2 * chunk;
+        const int4 a = t[0];
+        const int4 b = t[1];
+        k.off[0] = a.x;
+        k.shift[0] = a.y;
+        k.off[1] = a.z;
+        k.shift[1] = a.w;
+        k.off[2] = b.x;
+        k.shift[2] = b.y;
+        k.off[3] = b.z;
+        k.shift[3] = b.w;
+    }
+    else
+    {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+        {
+            k.off[q] = 0;
+            k.shift[q] = 0;
+        }
+    }
+    return k;
+}
+
 // Prologue of one key chunk (8 dims of a row whose 128 dims are spread over
 // 16 consecutive lanes, all active): per-head RMSNorm (fp32 sum of squares),
 // gamma, RoPE, bf16 rounding.
@@ -1101,8 +1154,8 @@ __device__ inline uint4 v_keys8_tr(const char* vr, int off)
 // rounding them again changes nothing) and store each column as one 16-byte
 // chunk.
 template <typename TI, int RM>
-__device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, const Staged& s, const RopeBase& rb,
-                                    char* smem, int kb, int wave, int lane)
+__device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, const Staged& s, char* smem, int kb,
+                                    int wave, int lane)
 {
     const int chunk = lane & 15;
     const int d0 = chunk * 8;
@@ -1113,7 +1166,7 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
         char* kt = k_tile(smem, p, kb);
         const int base = (kb - gm.ntb) * kBlockN;
         const int last = gm.vlen - 1;
-        const KeyRope kr = key_rope<RM>(rb, d0);
+        const KeyRope kr = staged_key_rope<RM>(p, smem, chunk);
 #pragma unroll
         for (int i = 0; i < 2; i++)
         {
@@ -1155,15 +1208,15 @@ __device__ inline void prepare_tile(const AttnParams& p, const Geometry& gm, con
 // fp32 inputs: waves 0-7 load tile kb into registers and prepare it into the
 // same LDS tiles (no raw copy in LDS).
 template <int RM>
-__device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry& gm, const Staged& s,
-                                             const RopeBase& rb, char* smem, int head, int kb, int tid)
+__device__ inline void load_prepare_tile_f32(const AttnParams& p, const Geometry& gm, const Staged& s, char* smem,
+                                             int head, int kb, int tid)
 {
     char* kt = k_tile(smem, p, kb);
     char* vt = vt_tile(smem, p, kb);
     const int r = tid >> 4;
     const int chunk = tid & 15;
     const int d0 = chunk * 8;
-    const KeyRope kr = key_rope<RM>(rb, d0);
+    const KeyRope kr = staged_key_rope<RM>(p, smem, chunk);
     if (kb < gm.ntb)
     {
         const int base = kb * kBlockN;
@@ -1543,6 +1596,7 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
         return;
 
     stage_window<RM>(p, box, smem, tid, kThreads);
+    stage_key_rope<RM>(p, box, smem, tid);
     __syncthreads();
     const Staged s = staged(p, smem);
 
@@ -1551,7 +1605,6 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     const bool wave_active = qbk.q0 + wave * 32 < qbk.q1;
     const int qrow = qbk.q0 + wave * 32 + lr;
     const int qrow_c = min(qrow, gm.seq - 1);
-    const RopeBase rb = rope_base(box);
     const ReadBases rdb = read_bases(lane);
 
     // the fetches of tiles 0 and 1 and the query loads are in flight together
@@ -1579,11 +1632,11 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
     {
         // tile 0 has landed once at most tile 1's fetches are outstanding
         wait_tile_fetch(wave, last_tile >= 1);
-        prepare_tile<TI, RM>(p, gm, s, rb, smem, 0, wave, lane);
+        prepare_tile<TI, RM>(p, gm, s, smem, 0, wave, lane);
     }
     else if (loader)
     {
-        load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, 0, tid);
+        load_prepare_tile_f32<RM>(p, gm, s, smem, head, 0, tid);
     }
     __syncthreads();
 
@@ -1607,7 +1660,7 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
             if (value_wave && kb + 1 < gm.nkb)
             {
                 __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-                prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+                prepare_tile<TI, RM>(p, gm, s, smem, kb + 1, wave, ln);
             }
             if (fetch)
                 dma_tile<TI>(p, gm, s, smem, head, kb + 2, wave, ln);
@@ -1630,12 +1683,12 @@ __global__ __launch_bounds__(kThreads) void window_attention_kernel(AttnParams p
                 if (!value_wave)
                 {
                     wait_tile_fetch(wave, fetch);
-                    prepare_tile<TI, RM>(p, gm, s, rb, smem, kb + 1, wave, ln);
+                    prepare_tile<TI, RM>(p, gm, s, smem, kb + 1, wave, ln);
                 }
             }
             else if (loader)
             {
-                load_prepare_tile_f32<RM>(p, gm, s, rb, smem, head, kb + 1, opaque(tid));
+                load_prepare_tile_f32<RM>(p, gm, s, smem, head, kb + 1, opaque(tid));
             }
         }
         __syncthreads();
@@ -2031,6 +2084,8 @@ LdsLayout lds_layout(int vmax, int rope_rows)
     off = align16(off + rope_rows * kRopePairSlots * 8);
     l.gamma = off;
     off += 2 * kHeadDim * 4;
+    l.krope = off;
+    off += 16 * 4 * 8;
     l.total = std::max(off, l.k + kWaves * 32 * kEpiStride);
     return l;
 }
@@ -2047,6 +2102,8 @@ LdsLayout lds_layout_staging(int vmax, int rope_rows)
     off = align16(off + rope_rows * kRopePairSlots * 8);
     l.gamma = off;
     off += 2 * kHeadDim * 4;
+    l.krope = off;
+    off += 16 * 4 * 8;
     l.total = off;
     return l;
 }
