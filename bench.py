@@ -204,41 +204,35 @@ def _gpu_ms(fn, reps=20):
     return a.elapsed_time(b) / reps
 
 
-def _row(name, variant, ms, flops, nbytes, cpu_ms, cores, err, passed):
+def _row(name, variant, ms, flops, nbytes):
     t = ms * 1e-3
     return {"config": name, "variant": variant, "gpu_ms": round(ms, 4), "tflops": round(flops / t / 1e12, 2),
             "mfma_pct": round(100 * flops / t / 1e12 / PEAK_FP16_TFLOPS, 2),
             "hbm_gbs": round(nbytes / t / 1e9, 1), "hbm_pct": round(100 * nbytes / t / 1e9 / PEAK_HBM_GBS, 2),
             "roofline_pct": round(100 * max(flops / (PEAK_FP16_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) / t, 2),
-            "cpu_ms": None if cpu_ms is None else round(cpu_ms, 1), "cpu_cores": cores, **err, "pass": passed}
+            "cpu_ms": None, "cpu_cores": None, "pass": None}
 
 
-def config_table(dev, with_cpu: bool):
-    """One row per configuration of the metric's config list that fits a GPU
-    and the CPU beside it: the single windowed MM-attention layer at the
-    480x256x5 grid 2x16x30 (config 1: fp32, no RoPE, no QK-norm, 2x8x10
-    unshifted windows; config 2: fp16, QK-RMSNorm + RoPE, unshifted and
+def config_table(dev):
+    """The GPU side of one row per configuration of the metric's config list
+    that fits a GPU and the CPU beside it: the single windowed MM-attention
+    layer at the 480x256x5 grid 2x16x30 (config 1: fp32, no RoPE, no QK-norm,
+    2x8x10 unshifted windows; config 2: fp16, QK-RMSNorm + RoPE, unshifted and
     shifted) and one DiT block at that grid (config 4: hidden 2560, 20 heads,
     MLP 6912, fp16 weights N(0, 0.02^2), fp16 inputs N(0, 1), 58 text tokens).
-    GPU ms: mean over 20 launches after 3 warmups (HIP events); CPU ms: the
-    oracle's median of 3 after a warmup, on the same inputs; errors of the
-    GPU outputs against the oracle's (the attention's gates: max-abs <= 2e-3
-    / mean-abs <= 2e-4 but for one-ulp bf16 flips; the block's: NRMSE <=
-    2e-3).  Config 3 is the line's own workload; config 5 the dit_step."""
+    GPU ms: mean over 20 launches after 3 warmups (HIP events).  Config 3 is
+    the line's own workload; config 5 the dit_step.
+
+    Returns the rows and, per row, the host inputs and GPU outputs that the
+    CPU-baseline leg (cpu_baseline_configs) times the oracle on and checks."""
     import torch
-    import oracle
     import sv2hip
-    from parity import cast_like, reference_freqs, report
+    from parity import cast_like, reference_freqs
     import ncnn_files as nf
-    oracle.load()
-    host = host_cpu()
-    threads = host["nproc"]
-    if host["omp_num_threads"]:
-        threads = min(threads, int(host["omp_num_threads"]))
     Tg, Hg, Wg, D = 2, 16, 30, HEADS * HD
     Lv = Tg * Hg * Wg
     freqs = reference_freqs()
-    rows = []
+    rows, cases = [], []
     tdt = {"f32": torch.float32, "f16": torch.float16}
     for name, in_dt, norm, rope, shifted in (("1", "f32", False, sv2hip.ROPE_NONE, False),
                                              ("2", "f16", True, sv2hip.ROPE_REFERENCE, False),
@@ -260,23 +254,13 @@ def config_table(dev, with_cpu: bool):
         ov = torch.empty((Lv, D), dtype=tdt[in_dt], device=dev)
         ot = torch.empty((L_TXT, D), dtype=tdt[in_dt], device=dev)
         ms = _gpu_ms(lambda: attn(tv, tt, tg, ov, ot))
-        ref = {}
-
-        def run_cpu():
-            ref["v"], ref["t"] = oracle.window_attention(vid, txt, Tg, Hg, Wg, heads=HEADS, qk_norm=norm,
-                                                         rope_mode=rope, freqs=freqs, gammas=gam, shifted=shifted,
-                                                         wt=2, wh=8, ww=10, threads=threads)
-        cpu_ms = _median_ms(run_cpu) if with_cpu else None
-        if not with_cpu:
-            run_cpu()
-        rep = report(ov.float().cpu().numpy(), cast_like(ref["v"], in_dt))
-        err = {"max_abs": rep["max_abs"], "mean_abs": rep["mean_abs"], "flips": rep["flips"]}
-        passed = bool(rep["finite"] and rep["over_tol_not_flip"] == 0 and rep["mean_abs"] <= 2e-4)
         rows.append(_row(name, f"2x8x10 {'shifted' if shifted else 'unshifted'}, "
                                f"{'no RoPE / no QK-norm' if not norm else 'QK-RMSNorm + reference RoPE'}, {in_dt}",
-                         ms, flops, nbytes, cpu_ms, threads, err, passed))
+                         ms, flops, nbytes))
+        cases.append(dict(kind="attention", gpu=ov.float().cpu().numpy(), vid=vid, txt=txt, grid=(Tg, Hg, Wg),
+                          in_dt=in_dt, norm=norm, rope=rope, freqs=freqs, gammas=gam, shifted=shifted))
 
-    # config 4: one block, fp16 compute, against the oracle's fp32 block
+    # config 4: one block, fp16 compute
     rng = np.random.default_rng(41)
     w = nf.random_weights(rng, D, DIT_FFN, shared=False)
     vid = rng.standard_normal((Lv, D), dtype=np.float32).astype(np.float16).astype(np.float32)
@@ -293,28 +277,56 @@ def config_table(dev, with_cpu: bool):
     ms = _gpu_ms(lambda: blk.forward(tv, tt, te, ov, ot, workspace=ws))
     gv = ov.float().cpu().numpy()
     blk.close()
-    ref = {}
-
-    def run_block():
-        ref["v"], ref["t"] = oracle.block_forward(w, vid, txt, emb, Tg, Hg, Wg, dim=D, heads=HEADS,
-                                                  mlp_hidden=DIT_FFN, shared=False, shifted=False, wt=2, wh=8, ww=10,
-                                                  threads=threads)
-    cpu_ms = _median_ms(run_block) if with_cpu else None
-    if not with_cpu:
-        run_block()
-    d = gv.astype(np.float64) - ref["v"]
-    rms = max(float(np.sqrt(np.mean(ref["v"].astype(np.float64) ** 2))), 1e-12)
-    nrmse = float(np.sqrt(np.mean(d * d))) / rms
-    rows_tok = Lv + L_TXT
-    gemm = 2.0 * rows_tok * D * (3 * D + D + 3 * DIT_FFN)
+    gemm = 2.0 * (Lv + L_TXT) * D * (3 * D + D + 3 * DIT_FFN)
     attn_f = sum(4.0 * (v + L_TXT) ** 2 * HD * HEADS for v in
                  [(x[1] - x[0]) * (x[3] - x[2]) * (x[5] - x[4])
                   for x in sv2hip.window_plan(sv2hip.rule(Tg, Hg, Wg, False, 2, 8, 10))])
     wbytes = 2 * 2 * (3 * D * D + D * D + 3 * D * DIT_FFN)  # two branches of fp16 matrices
-    err = {"max_abs": float(np.abs(d).max()), "mean_abs": float(np.abs(d).mean()), "nrmse": nrmse}
     rows.append(_row("4", "one block 960+58 tokens, 2x8x10 unshifted, fp16 (InnerProducts on hipBLASLt)",
-                     ms, gemm + attn_f, wbytes, cpu_ms, threads, err, bool(np.isfinite(gv).all() and nrmse <= 2e-3)))
-    return rows
+                     ms, gemm + attn_f, wbytes))
+    cases.append(dict(kind="block", gpu=gv, weights=w, vid=vid, txt=txt, emb=emb, grid=(Tg, Hg, Wg)))
+    return rows, cases
+
+
+def cpu_baseline_configs(rows, cases):
+    """The CPU-baseline leg of the per-configuration rows: the oracle's median
+    of 3 after a warmup on each row's inputs, on the host cores, and the
+    errors of the row's GPU outputs against the oracle's (the attention's
+    gates: max-abs <= 2e-3 / mean-abs <= 2e-4 but for one-ulp bf16 flips; the
+    block's, fp16 against the oracle's fp32 block: NRMSE <= 2e-3)."""
+    import oracle
+    from parity import cast_like, report
+    oracle.load()
+    host = host_cpu()
+    threads = host["nproc"]
+    if host["omp_num_threads"]:
+        threads = min(threads, int(host["omp_num_threads"]))
+    for row, c in zip(rows, cases):
+        T_, H_, W_ = c["grid"]
+        ref = {}
+        if c["kind"] == "attention":
+            def run():
+                ref["v"], ref["t"] = oracle.window_attention(
+                    c["vid"], c["txt"], T_, H_, W_, heads=HEADS, qk_norm=c["norm"], rope_mode=c["rope"],
+                    freqs=c["freqs"], gammas=c["gammas"], shifted=c["shifted"], wt=2, wh=8, ww=10, threads=threads)
+            cpu_ms = _median_ms(run)
+            rep = report(c["gpu"], cast_like(ref["v"], c["in_dt"]))
+            err = {"max_abs": rep["max_abs"], "mean_abs": rep["mean_abs"], "flips": rep["flips"]}
+            passed = bool(rep["finite"] and rep["over_tol_not_flip"] == 0 and rep["mean_abs"] <= 2e-4)
+        else:
+            D = HEADS * HD
+
+            def run():
+                ref["v"], ref["t"] = oracle.block_forward(c["weights"], c["vid"], c["txt"], c["emb"], T_, H_, W_,
+                                                          dim=D, heads=HEADS, mlp_hidden=DIT_FFN, shared=False,
+                                                          shifted=False, wt=2, wh=8, ww=10, threads=threads)
+            cpu_ms = _median_ms(run)
+            d = c["gpu"].astype(np.float64) - ref["v"]
+            rms = max(float(np.sqrt(np.mean(ref["v"].astype(np.float64) ** 2))), 1e-12)
+            nrmse = float(np.sqrt(np.mean(d * d))) / rms
+            err = {"max_abs": float(np.abs(d).max()), "mean_abs": float(np.abs(d).mean()), "nrmse": nrmse}
+            passed = bool(np.isfinite(c["gpu"]).all() and nrmse <= 2e-3)
+        row.update({"cpu_ms": round(cpu_ms, 1), "cpu_cores": threads, **err, "pass": passed})
 
 
 DIT_DIM, DIT_FFN, DIT_BLOCKS, LATENT_C, TEXT_C, OUT_C = 2560, 6912, 32, 33, 5120, 16
@@ -635,11 +647,14 @@ def main():
         result["config"]["dit_step"] = ds
         result["config"]["dit_step_cxx"] = dit_step_cxx(args.dit_steps)
     result["config"]["sampler_step"] = sampler_bench(dev)
-    if not args.no_table:
-        result["config"]["configs"] = config_table(dev, not args.no_cpu)
+    table = config_table(dev) if not args.no_table else None
+    if table is not None:
+        result["config"]["configs"] = table[0]
     result["config"]["hipblaslt_mapped"] = mapped_libraries("libhipblaslt")
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
+        if table is not None:
+            cpu_baseline_configs(*table)
     print(json.dumps(result))
 
 
