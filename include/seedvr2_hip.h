@@ -156,6 +156,26 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args);
  * element is rounded to bf16 as the reference rounds it (:1074). */
 int sv2_window_attention(const sv2_attn_args* args, void* stream);
 
+/* The three launches of sv2_window_attention, selectable (a bit set of the
+ * values below; SV2_ATTN_STAGE_ALL is sv2_window_attention):
+ *   SV2_ATTN_STAGE_TEXT_PREPARE  the text rows' q/k prologue and V, once per
+ *                                layer, into the workspace;
+ *   SV2_ATTN_STAGE_WINDOWS       the window attention kernel (video outputs,
+ *                                per-window text partials in the workspace);
+ *   SV2_ATTN_STAGE_TEXT_REDUCE   the text outputs from those partials.
+ * Each stage reads what the earlier ones left in the same workspace, so stages
+ * run in this order on one stream with the same args.  No counterpart in the
+ * reference (its Vulkan path records the three as one sequence): for callers
+ * that time or schedule the launches one at a time.  The exact mode accepts
+ * SV2_ATTN_STAGE_ALL only (SV2_EUNSUPPORTED otherwise). */
+enum sv2_attn_stage {
+    SV2_ATTN_STAGE_TEXT_PREPARE = 1,
+    SV2_ATTN_STAGE_WINDOWS = 2,
+    SV2_ATTN_STAGE_TEXT_REDUCE = 4,
+    SV2_ATTN_STAGE_ALL = 7
+};
+int sv2_window_attention_stages(const sv2_attn_args* args, int stages, void* stream);
+
 /* Device.  sv2_window_attention for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc); it has no counterpart in the reference.  args->workspace

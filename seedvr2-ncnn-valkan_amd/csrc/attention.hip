@@ -2228,15 +2228,21 @@ void launch_text_prepare(const AttnParams& p, hipStream_t stream)
     hipLaunchKernelGGL((text_prepare_kernel<TI, RM>), grid, dim3(256), 0, stream, p);
 }
 
+// stages: SV2_ATTN_STAGE_TEXT_PREPARE and / or SV2_ATTN_STAGE_WINDOWS.
 template <typename TI, int RM>
-int launch_attention(const AttnParams& p, hipStream_t stream)
+int launch_attention(const AttnParams& p, int stages, hipStream_t stream)
 {
     const int rc = set_dynamic_lds(reinterpret_cast<const void*>(&window_attention_kernel<TI, RM>), p.lds.total,
                                    "window attention: dynamic LDS attribute");
     if (rc != SV2_OK)
         return rc;
-    if (p.text_len > 0)
+    if (p.text_len > 0 && (stages & SV2_ATTN_STAGE_TEXT_PREPARE))
         launch_text_prepare<TI, RM>(p, stream);
+    if (!(stages & SV2_ATTN_STAGE_WINDOWS))
+    {
+        const hipError_t err = hipGetLastError();
+        return err == hipSuccess ? SV2_OK : hip_error(err, "text_prepare_kernel launch");
+    }
     const int groups = (p.npairs + 7) / 8;
     const unsigned grid = static_cast<unsigned>(groups) * 8u * static_cast<unsigned>(p.nqb);
     hipLaunchKernelGGL((window_attention_kernel<TI, RM>), dim3(grid), dim3(kThreads), p.lds.total, stream, p);
@@ -2245,13 +2251,13 @@ int launch_attention(const AttnParams& p, hipStream_t stream)
 }
 
 template <typename TI>
-int launch_rope(const AttnParams& p, int rope_mode, hipStream_t stream)
+int launch_rope(const AttnParams& p, int rope_mode, int stages, hipStream_t stream)
 {
     if (rope_mode == SV2_ROPE_REFERENCE)
-        return launch_attention<TI, SV2_ROPE_REFERENCE>(p, stream);
+        return launch_attention<TI, SV2_ROPE_REFERENCE>(p, stages, stream);
     if (rope_mode == SV2_ROPE_ABSOLUTE)
-        return launch_attention<TI, SV2_ROPE_ABSOLUTE>(p, stream);
-    return launch_attention<TI, SV2_ROPE_NONE>(p, stream);
+        return launch_attention<TI, SV2_ROPE_ABSOLUTE>(p, stages, stream);
+    return launch_attention<TI, SV2_ROPE_NONE>(p, stages, stream);
 }
 
 template <typename TO>
@@ -2412,10 +2418,12 @@ catch (...)
     return sv2::caught_exception("sv2_window_attention_workspace");
 }
 
-int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
+int sv2_window_attention_stages(const sv2_attn_args* args, int stages, void* stream_ptr)
 try
 {
     using namespace sv2;
+    if (stages <= 0 || (stages & ~SV2_ATTN_STAGE_ALL) != 0)
+        return set_error(SV2_EINVAL, "attention: stages must be a non-empty set of SV2_ATTN_STAGE_* bits");
     AttnParams p;
     int smax = 0, vmax = 0, rope_rows = 0;
     int rc = prepare(args, &p, &smax, &vmax, &rope_rows);
@@ -2423,23 +2431,28 @@ try
         return rc;
     if (!args->vid_out || (args->text_len > 0 && !args->txt_out))
         return set_error(SV2_EINVAL, "attention: null output pointer");
+    if (p.exact && stages != SV2_ATTN_STAGE_ALL)
+        return set_error(SV2_EUNSUPPORTED, "attention: the exact mode runs its stages together (SV2_ATTN_STAGE_ALL)");
     if ((rc = bind_workspace(args, &p)) != SV2_OK)
         return rc;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
 
+    const int launch_stages = stages & (SV2_ATTN_STAGE_TEXT_PREPARE | SV2_ATTN_STAGE_WINDOWS);
     if (p.exact)
         rc = launch_exact(p, workspace_layout(p), static_cast<char*>(args->workspace), args->rope_mode, smax, vmax,
                           rope_rows, stream);
+    else if (launch_stages == 0)
+        rc = SV2_OK;
     else if (args->qkv_dtype == SV2_F32)
-        rc = launch_rope<F32>(p, args->rope_mode, stream);
+        rc = launch_rope<F32>(p, args->rope_mode, launch_stages, stream);
     else if (args->qkv_dtype == SV2_F16)
-        rc = launch_rope<F16>(p, args->rope_mode, stream);
+        rc = launch_rope<F16>(p, args->rope_mode, launch_stages, stream);
     else
-        rc = launch_rope<BF16>(p, args->rope_mode, stream);
+        rc = launch_rope<BF16>(p, args->rope_mode, launch_stages, stream);
     if (rc != SV2_OK)
         return rc;
 
-    if (p.text_len > 0)
+    if (p.text_len > 0 && (stages & SV2_ATTN_STAGE_TEXT_REDUCE))
     {
         if (args->out_dtype == SV2_F32)
             launch_reduce<F32>(p, args->txt_out, stream);
@@ -2455,7 +2468,12 @@ try
 }
 catch (...)
 {
-    return sv2::caught_exception("sv2_window_attention");
+    return sv2::caught_exception("sv2_window_attention_stages");
+}
+
+int sv2_window_attention(const sv2_attn_args* args, void* stream_ptr)
+{
+    return sv2_window_attention_stages(args, SV2_ATTN_STAGE_ALL, stream_ptr);
 }
 
 int sv2_window_attention_no_alloc(const sv2_attn_args* args, void* stream_ptr)

@@ -23,6 +23,7 @@ SV2_EDEVICE = -100
 F32, F16, BF16 = 0, 1, 2
 ROPE_REFERENCE, ROPE_ABSOLUTE, ROPE_NONE = 0, 1, 2
 VERIFY_NONE, VERIFY_IF_PRESENT, VERIFY_STRICT = 0, 1, 2
+STAGE_TEXT_PREPARE, STAGE_WINDOWS, STAGE_TEXT_REDUCE, STAGE_ALL = 1, 2, 4, 7
 
 # Exported symbols declared in include/seedvr2_hip.h.
 EXPORTS = [
@@ -33,6 +34,7 @@ EXPORTS = [
     "sv2_rope_positions_needed",
     "sv2_window_attention_workspace",
     "sv2_window_attention",
+    "sv2_window_attention_stages",
     "sv2_window_attention_no_alloc",
     "sv2_qk_prologue",
     "sv2_rmsnorm_ada",
@@ -233,6 +235,8 @@ def load() -> ctypes.CDLL:
     lib.sv2_window_attention_workspace.restype = ctypes.c_int64
     lib.sv2_window_attention.argtypes = [ctypes.POINTER(AttnArgs), vp]
     lib.sv2_window_attention.restype = i
+    lib.sv2_window_attention_stages.argtypes = [ctypes.POINTER(AttnArgs), i, vp]
+    lib.sv2_window_attention_stages.restype = i
     lib.sv2_window_attention_no_alloc.argtypes = [ctypes.POINTER(AttnArgs), vp]
     lib.sv2_window_attention_no_alloc.restype = i
     lib.sv2_qk_prologue.argtypes = [ctypes.POINTER(AttnArgs), vp, vp, vp, vp]
@@ -470,10 +474,16 @@ class WindowAttention:
         a.workspace = None if need == 0 else self.workspace.data_ptr()
         a.workspace_bytes = need
 
-    def __call__(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
+    def __call__(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None, stages=None):
+        """All three launches (sv2_window_attention), or the STAGE_* bits of
+        `stages` through sv2_window_attention_stages."""
         a = self.args(vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre)
         self._bind_workspace(a, vid_qkv.device)
-        check(load().sv2_window_attention(ctypes.byref(a), _stream(stream)), "sv2_window_attention")
+        if stages is None:
+            check(load().sv2_window_attention(ctypes.byref(a), _stream(stream)), "sv2_window_attention")
+        else:
+            check(load().sv2_window_attention_stages(ctypes.byref(a), int(stages), _stream(stream)),
+                  "sv2_window_attention_stages")
 
     def run_no_alloc(self, vid_qkv, txt_qkv, gammas, vid_out, txt_out, debug_pre=None, stream=None):
         """The same attention through sv2_window_attention_no_alloc (the

@@ -133,6 +133,32 @@ def test_attention_argument_checks(hip):
     assert lib.sv2_window_attention(None, None) == hip.SV2_EINVAL
 
 
+def test_attention_stage_checks(hip):
+    """sv2_window_attention_stages takes a non-empty set of the three stage
+    bits, checks the arguments as sv2_window_attention does, and runs the
+    exact mode's stages only together; all rejected on the host."""
+    lib = hip.load()
+    a = hip.AttnArgs()
+    a.rule = hip.rule(2, 16, 30, False, 2, 8, 10)
+    a.heads, a.head_dim, a.text_len, a.eps = 20, 128, 58, 1e-5
+    a.rope_mode = hip.ROPE_NONE
+    a.qk_norm = 0
+    a.vid_qkv = a.txt_qkv = 16
+    a.qkv_dtype = a.out_dtype = hip.F16
+    for bad in (0, 8, 9, -1):
+        assert lib.sv2_window_attention_stages(ctypes.byref(a), bad, None) == hip.SV2_EINVAL, bad
+        assert b"stages" in lib.sv2_last_error()
+    # outputs missing: the same check as the combined call
+    assert lib.sv2_window_attention_stages(ctypes.byref(a), hip.STAGE_WINDOWS, None) == hip.SV2_EINVAL
+    assert b"output" in lib.sv2_last_error()
+    a.vid_out = a.txt_out = 16
+    a.qkv_dtype = a.out_dtype = hip.F32
+    a.exact = 1
+    for partial in (hip.STAGE_TEXT_PREPARE, hip.STAGE_WINDOWS, hip.STAGE_TEXT_REDUCE, 3, 6):
+        assert lib.sv2_window_attention_stages(ctypes.byref(a), partial, None) == hip.SV2_EUNSUPPORTED, partial
+    assert (hip.STAGE_TEXT_PREPARE | hip.STAGE_WINDOWS | hip.STAGE_TEXT_REDUCE) == hip.STAGE_ALL
+
+
 def test_workspace_size_formula(hip):
     """Per-window bf16 text partials, the prepared text q, k and v^T, and the
     first two text tiles' v^T per head in the attention kernel's LDS byte

@@ -168,3 +168,38 @@ def test_prologue_matches_oracle(hip, orc, device, rope_mode, in_dtype):
             d = np.abs(g[differ].astype(np.float64) - r[differ])
             ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(g[differ]), np.abs(r[differ])))[1] - 8)
             assert ((d <= ulp * 1.000001) | (d <= 1e-6)).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_stages_one_at_a_time_equal_the_combined_call(hip, device, dtype):
+    """sv2_window_attention_stages: the text prologue, the window kernel and
+    the text reduction launched one call each (and the first two together)
+    give the combined call's outputs bit for bit."""
+    import torch
+    print(f"[stages] {dtype}", flush=True)
+    T, H, W, heads = 2, 16, 30, 20
+    D = heads * 128
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    g = torch.Generator(device=device)
+    g.manual_seed(77)
+    vid = torch.randn((T * H * W, 3 * D), generator=g, device=device).to(tdt)
+    txt = torch.randn((L_TXT, 3 * D), generator=g, device=device).to(tdt)
+    gam = [torch.rand(128, generator=g, device=device) + 0.5 for _ in range(4)]
+    attn = hip.WindowAttention(hip.rule(T, H, W, True, 2, 8, 10), heads, L_TXT, freqs=reference_freqs(),
+                               device=device)
+
+    def outs():
+        return (torch.full((T * H * W, D), float("nan"), dtype=tdt, device=device),
+                torch.full((L_TXT, D), float("nan"), dtype=tdt, device=device))
+
+    ref_v, ref_t = outs()
+    attn(vid, txt, gam, ref_v, ref_t)
+    for split in ([hip.STAGE_TEXT_PREPARE, hip.STAGE_WINDOWS, hip.STAGE_TEXT_REDUCE],
+                  [hip.STAGE_TEXT_PREPARE | hip.STAGE_WINDOWS, hip.STAGE_TEXT_REDUCE]):
+        ov, ot = outs()
+        attn.workspace.fill_(255)  # the stages must rebuild what the combined call left there
+        for st in split:
+            attn(vid, txt, gam, ov, ot, stages=st)
+        torch.cuda.synchronize()
+        assert torch.equal(ov, ref_v), split
+        assert torch.equal(ot, ref_t), split
