@@ -446,6 +446,62 @@ def dit_bench(dev, steps: int, warmup: int):
     }
 
 
+def elementwise_bench(dev, reps: int = 20):
+    """The block's row-wise kernels at the 720p x 21f DiT shape (21600 video +
+    58 text rows, merged as in the shared-weight blocks; hidden 2560, MLP
+    6912; fp16 rows, fp32 modulation vectors): per kernel the mean device time
+    of `reps` launches captured in one HIP graph and its algorithmic HBM bytes
+    (each element read and written once: RMSNorm + ada 2 + 2 B, the gated
+    residual in place 2 + 2 + 2 B, SwiGLU in place 2 + 2 + 2 B).  The in-place
+    kernels run on values kept bounded (|gate| < 1, value in [0.5, 1))."""
+    import torch
+    import sv2hip
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    rows, D, F = T * H * W + L_TXT, DIT_DIM, DIT_FFN
+    f16 = torch.float16
+    x = torch.randn((rows, D), generator=g, device=dev).to(f16)
+    y = torch.empty_like(x)
+    res = torch.randn((rows, D), generator=g, device=dev).to(f16)
+    emb = torch.randn(6 * D, generator=g, device=dev) * 0.02
+    shift = torch.randn(D, generator=g, device=dev) * 0.02
+    scale = torch.randn(D, generator=g, device=dev) * 0.02
+    gate_vec = torch.rand(D, generator=g, device=dev) * 0.5
+    hx = torch.randn((rows, F), generator=g, device=dev).to(f16)
+    hv = (torch.rand((rows, F), generator=g, device=dev) * 0.5 + 0.5).to(f16)
+    cur = torch.cuda.current_stream
+    ops = {
+        "rmsnorm_ada": (lambda: sv2hip.rmsnorm_ada(x, y, 1e-5, emb, shift, scale, 0, True, stream=cur()),
+                        rows * D * 4),
+        "ada_residual": (lambda: sv2hip.ada_residual(y, res, emb, gate_vec, 0, 0, stream=cur()), rows * D * 6),
+        "swiglu": (lambda: sv2hip.swiglu(hx, hv, stream=cur()), rows * F * 6),
+    }
+    out = {}
+    for name, (fn, nbytes) in ops.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur())
+        graph.replay()
+        b.record(cur())
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / us / 1e3, 1),
+                     "hbm_util": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
+        del graph
+    out["workload"] = ("row-wise kernels at 1280x720x21: 21658 rows x 2560 (RMSNorm + ada, gated residual) and "
+                       "21658 x 6912 (SwiGLU), fp16")
+    return out
+
+
 def sampler_bench(dev, reps: int = 50):
     """The sampler half of one Euler step at 1280x720x21 (latent 16x6x90x160,
     fp32, resident): the 33-channel DiT input, CFG 6.5 with rescale 0.7 of two
@@ -519,6 +575,8 @@ def main():
     ap.add_argument("--dit-steps", type=int, default=3, help="timed DiT forwards (0 skips the DiT leg)")
     ap.add_argument("--dit-only", action="store_true",
                     help="run only the DiT leg and print its figures (for profiling the DiT step)")
+    ap.add_argument("--elementwise-only", action="store_true",
+                    help="run only the row-wise kernels' leg and print its figures (for profiling them)")
     ap.add_argument("--sampler-only", action="store_true",
                     help="run only the sampler leg and print its figures (for profiling the sampler kernels)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -543,6 +601,9 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
         return
     sv2hip.load()
+    if args.elementwise_only:
+        print(json.dumps({"elementwise": elementwise_bench(dev)}))
+        return
     if args.sampler_only:
         print(json.dumps({"sampler_step": sampler_bench(dev)}))
         return
@@ -666,6 +727,7 @@ def main():
         result["config"]["dit_step"] = ds
         result["config"]["dit_step_cxx"] = dit_step_cxx(args.dit_steps)
     result["config"]["sampler_step"] = sampler_bench(dev)
+    result["config"]["elementwise"] = elementwise_bench(dev)
     table = config_table(dev) if not args.no_table else None
     if table is not None:
         result["config"]["configs"] = table[0]

@@ -506,6 +506,81 @@ int launch_rmsnorm(const void* x, void* y, int dtype, int rows, int dim, float e
     return err == hipSuccess ? SV2_OK : hip_error(err, "rmsnorm_ada_kernel launch");
 }
 
+// Mode 0 with the gate read from emb (the sv2_ada_residual entry point):
+// x = x * (emb[c*6+slot] + gate[c]) + residual.  emb's gate column is strided
+// (6 floats per channel), so the workgroup forms the channel gates once in
+// LDS for kResidualRows rows instead of every lane reading them from L2 per
+// element; the rows then stream through with 16-byte accesses.
+constexpr int kResidualRows = 16;
+constexpr int kResidualMaxDim = 16384; // LDS for the staged gates: dim floats
+
+template <typename T>
+__global__ __launch_bounds__(256) void ada_residual_emb_kernel(void* x, const void* residual, int rows, int dim,
+                                                               const float* emb, const float* gate, int slot)
+{
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float g[];
+    for (int c = threadIdx.x; c < dim; c += 256)
+        g[c] = emb[c * 6 + slot] + gate[c];
+    __syncthreads();
+    const int r0 = blockIdx.x * kResidualRows;
+    const int nr = min(kResidualRows, rows - r0);
+    const int chunks = dim / 8;
+    // item j of the workgroup: row r0 + rr, channels cc * 8 ..; walked with
+    // the row and chunk stepped incrementally (no division per item)
+    int rr = 0;
+    int cc = threadIdx.x;
+    while (cc >= chunks)
+    {
+        cc -= chunks;
+        rr++;
+    }
+    while (rr < nr)
+    {
+        const int c0 = cc * 8;
+        const long long i = static_cast<long long>(r0 + rr) * dim + c0;
+        float a[8];
+        float r[8];
+        ld8<T>(x, i, a);
+        ld8<T>(residual, i, r);
+        const float4 g0 = *reinterpret_cast<const float4*>(&g[c0]);
+        const float4 g1 = *reinterpret_cast<const float4*>(&g[c0 + 4]);
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            const float t = a[e] * gg[e];
+            out[e] = t + r[e];
+        }
+        st8<T>(x, i, out);
+        cc += 256;
+        while (cc >= chunks)
+        {
+            cc -= chunks;
+            rr++;
+        }
+    }
+}
+
+int launch_residual_emb(void* x, const void* residual, int dtype, int rows, int dim, const float* emb,
+                        const float* gate, int slot, hipStream_t stream)
+{
+    const dim3 grid(static_cast<unsigned>((rows + kResidualRows - 1) / kResidualRows));
+    const size_t lds = static_cast<size_t>(dim) * sizeof(float);
+    if (dtype == SV2_F32)
+        hipLaunchKernelGGL((ada_residual_emb_kernel<F32>), grid, dim3(256), lds, stream, x, residual, rows, dim, emb,
+                           gate, slot);
+    else if (dtype == SV2_F16)
+        hipLaunchKernelGGL((ada_residual_emb_kernel<F16>), grid, dim3(256), lds, stream, x, residual, rows, dim, emb,
+                           gate, slot);
+    else
+        hipLaunchKernelGGL((ada_residual_emb_kernel<BF16>), grid, dim3(256), lds, stream, x, residual, rows, dim, emb,
+                           gate, slot);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? SV2_OK : hip_error(err, "ada_residual_emb_kernel launch");
+}
+
 template <typename Gate>
 int launch_residual(void* x, const void* residual, int dtype, int rows, int dim, Gate gate, const float* bias,
                     int mode, hipStream_t stream)
@@ -602,6 +677,9 @@ try
         return set_error(SV2_EINVAL, "ada_residual: null pointer");
     if (slot_base != 0 && slot_base != 3)
         return set_error(SV2_EINVAL, "ada_residual: slot_base must be 0 or 3");
+    if (mode == 0 && dim <= kResidualMaxDim)
+        return launch_residual_emb(x, residual, io_dtype, rows, dim, emb, gate_vec, slot_base + 2,
+                                   static_cast<hipStream_t>(stream_ptr));
     const EmbGate gate{emb, gate_vec, slot_base + 2};
     return launch_residual(x, residual, io_dtype, rows, dim, gate, nullptr, mode, static_cast<hipStream_t>(stream_ptr));
 }

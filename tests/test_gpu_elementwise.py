@@ -99,6 +99,27 @@ def test_ada_residual(hip, orc, device, dtype, mode):
     check(tx.float().cpu().numpy(), ref, dtype, 1 if dtype == "f32" else 1)
 
 
+@pytest.mark.parametrize("rows,dim", [(1, 8), (17, 136), (33, 24), (5, 16384), (3, 16392)],
+                         ids=["one-row", "dim136", "dim24", "dim16384", "dim16392-flat"])
+def test_ada_residual_gate_shapes(hip, orc, device, rows, dim):
+    # mode 0 stages the channel gates in LDS per 16-row workgroup up to dim
+    # 16384 (wider rows take the per-element kernel): ragged last workgroups,
+    # rows narrower than one pass of the 256 lanes, the largest staged dim
+    # and the first unstaged one, all in the oracle's order
+    print(f"[ada_residual gate] rows={rows} dim={dim}", flush=True)
+    rng = np.random.default_rng(rows * 7 + dim)
+    x = cast_like(rng.standard_normal((rows, dim)).astype(np.float32), "f16")
+    r = cast_like(rng.standard_normal((rows, dim)).astype(np.float32), "f16")
+    emb = rng.standard_normal(6 * dim).astype(np.float32)
+    gate = (rng.standard_normal(dim) * 0.02).astype(np.float32)
+    ref = orc.ada_output_residual(x, r, emb, gate, 3)
+    tx = dev(x, "f16", device)
+    tr = dev(r, "f16", device)
+    hip.ada_residual(tx, tr, torch.from_numpy(emb).to(device), torch.from_numpy(gate).to(device), 3, 0)
+    torch.cuda.synchronize()
+    check(tx.float().cpu().numpy(), ref, "f16", 1)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 def test_swiglu(hip, orc, device, dtype):
     print(f"[swiglu] {dtype}", flush=True)
