@@ -502,6 +502,92 @@ def elementwise_bench(dev, reps: int = 20):
     return out
 
 
+def text_products_bench(dev):
+    """The text branch's four InnerProducts at 58 rows (the DiT's text tokens;
+    hidden 2560, MLP 6912, fp16): the few-row kernel with its pass fused
+    (sv2_inner_product_f16_few) against torch.matmul (hipBLASLt) plus the
+    separate pass the library path runs after it (proj: the gated residual;
+    gate/in: SwiGLU; the out product's gated residual rides in the library's
+    epilogue, so its library figure is the product alone).  Weights are
+    rotated over copies of at least 700 MB so every launch streams its weight
+    matrix from HBM, as each block's does in a forward; mean device time of
+    3 launches per copy, replayed from a HIP graph."""
+    import math
+    import torch
+    import sv2hip
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(58)
+    M, D, F = L_TXT, DIT_DIM, DIT_FFN
+    f16 = torch.float16
+    cur = torch.cuda.current_stream
+    emb = torch.randn(6 * D, generator=g, device=dev) * 0.02
+    gate_vec = torch.rand(D, generator=g, device=dev) * 0.5
+    bias = torch.randn(D, generator=g, device=dev) * 0.02
+    lib = sv2hip.load()
+    ws = torch.empty(16 << 20, dtype=torch.uint8, device=dev)
+
+    def timed(fn, reps):
+        # captured in one HIP graph, so host launch overhead does not enter
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(reps):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur())
+        graph.replay()
+        b.record(cur())
+        torch.cuda.synchronize()
+        del graph
+        return a.elapsed_time(b) * 1e3 / reps
+
+    out = {}
+    for name, K, N, epi in (("qkv", D, 3 * D, sv2hip.EPI_STORE), ("proj", D, D, sv2hip.EPI_RESIDUAL),
+                            ("gate_in", D, F, sv2hip.EPI_SWIGLU), ("out", F, D, sv2hip.EPI_RESIDUAL)):
+        nw = 2 if epi == sv2hip.EPI_SWIGLU else 1
+        wbytes = N * K * 2 * nw
+        R = max(4, math.ceil(700e6 / wbytes))
+        x = torch.randn((M, K), generator=g, device=dev).to(f16)
+        w1 = [(torch.randn((N, K), generator=g, device=dev) * 0.02).to(f16) for _ in range(R)]
+        w2 = [(torch.randn((N, K), generator=g, device=dev) * 0.02).to(f16) for _ in range(R)] if nw == 2 else None
+        res = torch.randn((M, N), generator=g, device=dev).to(f16)
+        y = torch.empty((M, N), dtype=f16, device=dev)
+        y2 = torch.empty_like(y)
+        gt = gate_vec[:N] if N == D else None
+        bs = bias if name == "proj" else None
+
+        def few(i):
+            sv2hip.inner_product_f16_few(x, w1[i % R], y, epi, w_value=w2[i % R] if w2 else None,
+                                         bias=bs, gate=gt if epi == sv2hip.EPI_RESIDUAL else None,
+                                         residual=res if epi == sv2hip.EPI_RESIDUAL else None, workspace=ws,
+                                         stream=cur())
+
+        def library(i):
+            torch.matmul(x, w1[i % R].t(), out=y)
+            if name == "proj":
+                sv2hip.ada_residual(y, res, emb, gate_vec, 0, 0, stream=cur())
+            elif name == "gate_in":
+                torch.matmul(x, w2[i % R].t(), out=y2)
+                sv2hip.swiglu(y, y2, stream=cur())
+
+        t_few = timed(few, 3 * R)
+        t_lib = timed(library, 3 * R)
+        out[name] = {"in": K, "out": N, "weight_mb": round(wbytes / 1e6, 1), "few_us": round(t_few, 2),
+                     "library_us": round(t_lib, 2), "few_gbs": round(wbytes / t_few / 1e3, 1),
+                     "splits": int(max(1, lib.sv2_inner_product_f16_few_workspace(M, K, N, epi)
+                                       // max(1, M * N * 4)))}
+        del w1, w2
+        torch.cuda.empty_cache()
+    out["workload"] = ("text-branch InnerProducts at 58 rows (2560 -> 7680; 2560 -> 2560 + gated residual; "
+                       "2560 -> 2 x 6912 + SwiGLU; 6912 -> 2560 + gated residual), fp16, weights from HBM")
+    return out
+
+
 def sampler_bench(dev, reps: int = 50):
     """The sampler half of one Euler step at 1280x720x21 (latent 16x6x90x160,
     fp32, resident): the 33-channel DiT input, CFG 6.5 with rescale 0.7 of two
@@ -577,6 +663,8 @@ def main():
                     help="run only the DiT leg and print its figures (for profiling the DiT step)")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="run only the row-wise kernels' leg and print its figures (for profiling them)")
+    ap.add_argument("--text-products-only", action="store_true",
+                    help="run only the text-branch InnerProducts' leg and print its figures")
     ap.add_argument("--sampler-only", action="store_true",
                     help="run only the sampler leg and print its figures (for profiling the sampler kernels)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -606,6 +694,9 @@ def main():
         return
     if args.sampler_only:
         print(json.dumps({"sampler_step": sampler_bench(dev)}))
+        return
+    if args.text_products_only:
+        print(json.dumps({"text_products": text_products_bench(dev)}))
         return
     if args.dit_only:
         print(json.dumps({"dit_step": dit_bench(dev, max(args.dit_steps, 1), 1)}))
@@ -728,6 +819,7 @@ def main():
         result["config"]["dit_step_cxx"] = dit_step_cxx(args.dit_steps)
     result["config"]["sampler_step"] = sampler_bench(dev)
     result["config"]["elementwise"] = elementwise_bench(dev)
+    result["config"]["text_products"] = text_products_bench(dev)
     table = config_table(dev) if not args.no_table else None
     if table is not None:
         result["config"]["configs"] = table[0]

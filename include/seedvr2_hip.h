@@ -526,6 +526,24 @@ void sv2_dit_destroy(sv2_dit* dit);
 int sv2_inner_product_f16(const void* x, const void* w, const void* w_value, void* y, int rows, int in, int out,
                           int epilogue, const float* bias, const float* gate, const void* residual, void* stream);
 
+/* ---- The same InnerProducts and fused passes for 1-64 rows (the text
+ * branch's tokens: seedvr2_dit_block.cpp:1155-1156, :1180-1181, :1101,
+ * :1111 on the text rows), on a weight-streaming kernel: each weight is read
+ * once, whole 128-byte lines straight into LDS, K split over workgroups when
+ * the output columns alone give too few.  Epilogues as sv2_inner_product_f16;
+ * SV2_EPI_STORE also takes an optional bias: y = fp16(fp16(x W^T) + bias).
+ * Requires 1 <= rows <= 64, in % 64 == 0 and out % 64 == 0 (SV2_EPI_SWIGLU:
+ * out % 32 == 0, no bias or gate); SV2_EUNSUPPORTED otherwise.  When K is
+ * split the partial sums go to `workspace` (device memory of at least
+ * sv2_inner_product_f16_few_workspace() bytes; 0 bytes: none needed, NULL
+ * allowed); they are added in a fixed order, so results do not depend on
+ * timing.  Calls that share a workspace must not overlap.  y may not alias
+ * x, W, residual or the workspace. */
+int64_t sv2_inner_product_f16_few_workspace(int rows, int in, int out, int epilogue);
+int sv2_inner_product_f16_few(const void* x, const void* w, const void* w_value, void* y, int rows, int in, int out,
+                              int epilogue, const float* bias, const float* gate, const void* residual,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- fp32 InnerProduct of the parity mode.  Replaces the block's ncnn
  * InnerProduct layers (load_inner_product, seedvr2_dit_block.cpp:27-55) and
  * the heads' (seedvr2_dit_input.cpp:354-392, seedvr2_dit_output.cpp:388-390)

@@ -13,6 +13,7 @@
 #include "ncnn_format.h"
 #include "sv2_internal.h"
 
+using sv2::gemm_few;
 using sv2::gemm_mfma;
 using sv2::gemm_rows;
 using sv2::gemm_rows_bias;
@@ -255,11 +256,23 @@ sv2_attn_args attention_args(const sv2_block* b, int text_len)
 }
 
 // Workspace regions (bytes, 256-aligned): xa / m [R, D], qkv [R, 3D], att [R, D],
-// p_v [Lv, D], p_t [Lt, D], g and u [R, F], attention workspace; R = max(Lv, Lt).
+// p_v [Lv, D], p_t [Lt, D], g and u [R, F], the few-row InnerProducts' partial
+// sums (fp16 text rows), attention workspace; R = max(Lv, Lt).
 struct BlockWorkspace
 {
-    size_t tables, xa, qkv_v, qkv_t, att_v, att_t, p_v, p_t, g, u, attn, total;
+    size_t tables, xa, qkv_v, qkv_t, att_v, att_t, p_v, p_t, g, u, few, few_bytes, attn, total;
 };
+
+// The text branch's InnerProducts run on the few-row kernel (gemm_few.hip)
+// when the compute type is fp16 and every one of its shapes fits it.
+bool few_text_products(const sv2_block* b, int text_len)
+{
+    using namespace sv2;
+    const int D = b->cfg.dim, F = b->cfg.mlp_hidden;
+    return b->dtype == SV2_F16 && gemm_few_supported(text_len, D, 3 * D, kGemmStore) &&
+           gemm_few_supported(text_len, D, D, kGemmResidual) && gemm_few_supported(text_len, D, F, kGemmSwiGLU) &&
+           gemm_few_supported(text_len, F, D, kGemmResidual);
+}
 
 size_t align256(size_t v)
 {
@@ -313,6 +326,16 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
     off = align256(off + R * F * es);
     w->u = off;
     off = align256(off + R * F * es);
+    w->few = off;
+    w->few_bytes = 0;
+    if (few_text_products(b, text_len))
+    {
+        const int d = b->cfg.dim, f = b->cfg.mlp_hidden;
+        w->few_bytes = std::max({sv2::gemm_few_workspace(text_len, d, 3 * d, sv2::kGemmStore),
+                                 sv2::gemm_few_workspace(text_len, d, d, sv2::kGemmResidual),
+                                 sv2::gemm_few_workspace(text_len, f, d, sv2::kGemmResidual)});
+    }
+    off = align256(off + w->few_bytes);
     w->attn = off;
     off = align256(off + static_cast<size_t>(attn));
     w->total = off;
@@ -322,9 +345,12 @@ int workspace_layout(const sv2_block* b, int text_len, BlockWorkspace* w)
 // The MLP of one branch on rows [rows, D]: RMSNorm + ada (mlp shift/scale),
 // gate and in InnerProducts, SwiGLU, out InnerProduct, gated residual with x
 // (seedvr2_dit_block.cpp:1093-1112, :1211-1223, :1248-1260).  `table` is the
-// branch's MLP modulation table.
+// branch's MLP modulation table.  `fused`: the hand-written MFMA products
+// with their passes fused in; `few` (text rows): the few-row kernel, the
+// same fusion, partial sums in few_ws.
 int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, const float* table, const void* x,
-               int rows, void* out, char* m, char* g, char* u, bool fused)
+               int rows, void* out, char* m, char* g, char* u, bool fused, bool few = false, char* few_ws = nullptr,
+               size_t few_bytes = 0)
 {
     using namespace sv2;
     if (rows == 0)
@@ -342,6 +368,14 @@ int branch_mlp(const sv2_block* b, hipStream_t stream, const DevBranch& br, cons
                             nullptr)) != SV2_OK)
             return rc;
         return gemm_mfma(stream, rows, F, D, g, br.w_out, nullptr, out, kGemmResidual, nullptr, table + 2 * D, x);
+    }
+    if (few)
+    {
+        if ((rc = gemm_few(stream, rows, D, F, m, br.w_gate, br.w_in, g, kGemmSwiGLU, nullptr, nullptr, nullptr,
+                           few_ws, few_bytes)) != SV2_OK)
+            return rc;
+        return gemm_few(stream, rows, F, D, g, br.w_out, nullptr, out, kGemmResidual, nullptr, table + 2 * D, x,
+                        few_ws, few_bytes);
     }
     if ((rc = gemm_rows(stream, dt, rows, D, F, m, br.w_gate, g)) != SV2_OK ||
         (rc = gemm_rows(stream, dt, rows, D, F, m, br.w_in, u)) != SV2_OK)
@@ -675,6 +709,9 @@ try
                         p_t == p_v + Lv * row_bytes;
     const int Lr = merged ? Lv + Lt : Lv; // rows of the video branch's row-wise steps
     b->last_merged = merged ? 1 : 0;
+    // unmerged fp16 text rows (at most 64) take the few-row InnerProducts
+    // with their passes fused; debug captures need the separate passes
+    const bool few = Lt > 0 && !merged && !dbg && few_text_products(b, Lt);
     if (Lt > 0 && !merged &&
         ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
          (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
@@ -713,7 +750,9 @@ try
         if ((rc = launch_rmsnorm_table(txt, xa, dt, Lt, D, c.norm_eps, tab_ta, tb.ada[0], nullptr,
                                        c.last_layer ? 0 : 1, stream)) != SV2_OK)
             return rc;
-        if ((rc = gemm_rows(stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
+        if ((rc = few ? gemm_few(stream, Lt, D, 3 * D, xa, tb.w_qkv, nullptr, qkv_t, kGemmStore, nullptr, nullptr,
+                                 nullptr, ws + w.few, w.few_bytes)
+                      : gemm_rows(stream, dt, Lt, D, 3 * D, xa, tb.w_qkv, qkv_t)) != SV2_OK)
             return rc;
         if (dbg && (rc = capture(dbg->qkv_txt, qkv_t, Lt, 3 * D)) != SV2_OK)
             return rc;
@@ -787,7 +826,15 @@ try
                 return rc;
         }
     }
-    if (Lt > 0 && !merged)
+    if (Lt > 0 && !merged && few)
+    {
+        // proj_out of the text rows with its bias and the (gated, or on the
+        // last layer plain) residual in the epilogue (:1180-1209)
+        if ((rc = gemm_few(stream, Lt, D, D, att_t, tb.w_proj, nullptr, p_t, kGemmResidual, tb.b_proj,
+                           c.last_layer ? nullptr : tab_ta + 2 * D, txt, ws + w.few, w.few_bytes)) != SV2_OK)
+            return rc;
+    }
+    else if (Lt > 0 && !merged)
     {
         if ((rc = gemm_rows_bias(stream, dt, Lt, D, D, att_t, tb.w_proj, tbias_in_product, p_t)) != SV2_OK)
             return rc;
@@ -812,7 +859,8 @@ try
             if ((rc = launch_residual_table(txt_out, nullptr, dt, Lt, D, nullptr, nullptr, 2, stream)) != SV2_OK)
                 return rc;
         }
-        else if ((rc = branch_mlp(b, stream, tb, tab_tm, p_t, Lt, txt_out, xa, g, u, false)) != SV2_OK)
+        else if ((rc = branch_mlp(b, stream, tb, tab_tm, p_t, Lt, txt_out, xa, g, u, false, few, ws + w.few,
+                                  w.few_bytes)) != SV2_OK)
         {
             return rc;
         }

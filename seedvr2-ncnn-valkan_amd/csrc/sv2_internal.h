@@ -179,6 +179,17 @@ bool gemm_mfma_supported(int in, int out, int epi);
 int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, const void* w2, void* y,
               int epi, const float* bias, const float* gate, const void* residual);
 
+// fp16 y = epilogue(x W^T) for 1-64 rows on the weight-streaming kernel
+// (gemm_few.hip), the same epilogues as gemm_mfma (kGemmStore also takes an
+// optional bias: y = fp16(fp16(x W^T) + bias)).  Needs in % 64 == 0 and
+// out % 64 == 0 (SwiGLU: out % 32 == 0).  K may be split over workgroups:
+// `work` then holds gemm_few_workspace() bytes of fp32 partial sums.
+bool gemm_few_supported(int rows, int in, int out, int epi);
+int gemm_few_splits(int rows, int in, int out, int epi);
+size_t gemm_few_workspace(int rows, int in, int out, int epi);
+int gemm_few(hipStream_t stream, int rows, int in, int out, const void* x, const void* w, const void* w2, void* y,
+             int epi, const float* bias, const float* gate, const void* residual, void* work, size_t work_bytes);
+
 // Allocates device memory for `count` host fp32 values, stores them as dtype
 // (SV2_F32 or SV2_F16, round to nearest) and records the allocation in *owned.
 int upload_weights(std::vector<void*>* owned, const float* host, size_t count, int dtype, const void** dev);

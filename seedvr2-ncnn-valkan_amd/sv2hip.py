@@ -77,6 +77,8 @@ EXPORTS = [
     "sv2_dit_forward",
     "sv2_dit_destroy",
     "sv2_inner_product_f16",
+    "sv2_inner_product_f16_few_workspace",
+    "sv2_inner_product_f16_few",
     "sv2_inner_product_f32",
     "sv2_euler_timesteps",
     "sv2_condition_ratio",
@@ -327,6 +329,10 @@ def load() -> ctypes.CDLL:
     lib.sv2_dit_destroy.restype = None
     lib.sv2_inner_product_f16.argtypes = [vp, vp, vp, vp, i, i, i, i, vp, vp, vp, vp]
     lib.sv2_inner_product_f16.restype = i
+    lib.sv2_inner_product_f16_few_workspace.argtypes = [i, i, i, i]
+    lib.sv2_inner_product_f16_few_workspace.restype = ctypes.c_int64
+    lib.sv2_inner_product_f16_few.argtypes = [vp, vp, vp, vp, i, i, i, i, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.sv2_inner_product_f16_few.restype = i
     lib.sv2_inner_product_f32.argtypes = [vp, vp, vp, vp, i, i, i, vp]
     lib.sv2_inner_product_f32.restype = i
     i64 = ctypes.c_int64
@@ -1050,6 +1056,36 @@ def inner_product_f16(x, w, y, epilogue=EPI_STORE, w_value=None, bias=None, gate
     check(load().sv2_inner_product_f16(_ptr(x), _ptr(w), _ptr(w_value), _ptr(y), rows, k, out, epilogue,
                                        _ptr(bias), _ptr(gate), _ptr(residual), _stream(stream)),
           "sv2_inner_product_f16")
+    return y
+
+
+def inner_product_f16_few(x, w, y, epilogue=EPI_STORE, w_value=None, bias=None, gate=None, residual=None,
+                          workspace=None, stream=None):
+    """y = epilogue(x W^T) for 1-64 rows on the weight-streaming kernel
+    (sv2_inner_product_f16_few); arguments as inner_product_f16.  `workspace`
+    (a device tensor) receives the split partial sums; when None one of the
+    size sv2_inner_product_f16_few_workspace asks for is allocated here."""
+    import torch
+    rows, k = x.shape
+    out = w.shape[0]
+    for name, t, shape in (("x", x, (rows, k)), ("w", w, (out, k)), ("y", y, (rows, out))):
+        if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float16 and tuple(t.shape) == shape):
+            raise ValueError(f"{name} must be a contiguous fp16 device tensor {shape}")
+    for name, t, dt, shape in (("w_value", w_value, torch.float16, (out, k)), ("bias", bias, torch.float32, (out,)),
+                               ("gate", gate, torch.float32, (out,)),
+                               ("residual", residual, torch.float16, (rows, out))):
+        if t is not None and not (t.is_cuda and t.is_contiguous() and t.dtype == dt and tuple(t.shape) == shape):
+            raise ValueError(f"{name} must be a contiguous {dt} device tensor {shape}")
+    lib = load()
+    need = check(lib.sv2_inner_product_f16_few_workspace(rows, k, out, epilogue),
+                 "sv2_inner_product_f16_few_workspace")
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.sv2_inner_product_f16_few(_ptr(x), _ptr(w), _ptr(w_value), _ptr(y), rows, k, out, epilogue,
+                                        _ptr(bias), _ptr(gate), _ptr(residual), _ptr(workspace), ws_bytes,
+                                        _stream(stream)),
+          "sv2_inner_product_f16_few")
     return y
 
 

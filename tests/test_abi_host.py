@@ -227,3 +227,39 @@ def test_inner_product_argument_checks(hip):
     assert f32(p, p, None, p, -1, 16, 16, None) == hip.SV2_EINVAL
     assert f32(None, p, None, p, 4, 16, 16, None) == hip.SV2_EINVAL
     assert f32(None, None, None, None, 0, 16, 16, None) == hip.SV2_OK
+
+
+def test_few_row_inner_product_checks(hip):
+    """The few-row fp16 InnerProduct (sv2_inner_product_f16_few) checks its
+    shape, epilogue, pointers and workspace before any launch, and sizes its
+    split partial sums: 6 splits of 58 x 2560 fp32 for the 2560 -> 2560 and
+    6912 -> 2560 products (40 column tiles), 2 of 58 x 7680 for 2560 -> 7680
+    (120 tiles), none for SwiGLU."""
+    lib = hip.load()
+    ws = lib.sv2_inner_product_f16_few_workspace
+    assert ws(58, 2560, 2560, hip.EPI_RESIDUAL) == 6 * 58 * 2560 * 4
+    assert ws(58, 6912, 2560, hip.EPI_RESIDUAL) == 6 * 58 * 2560 * 4
+    assert ws(58, 2560, 7680, hip.EPI_STORE) == 2 * 58 * 7680 * 4
+    assert ws(58, 2560, 6912, hip.EPI_SWIGLU) == 0
+    assert ws(1, 64, 64, hip.EPI_STORE) == 0          # one K block: never split
+    assert ws(0, 2560, 2560, hip.EPI_STORE) == 0
+    assert ws(65, 2560, 2560, hip.EPI_STORE) == hip.SV2_EUNSUPPORTED
+    assert ws(58, 2560, 2560, 9) == hip.SV2_EINVAL
+    p = 16  # a non-null dummy address: every case below returns before touching it
+    f = lib.sv2_inner_product_f16_few
+    args = (None, None, None, None)
+    assert f(p, p, None, p, 65, 64, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_EUNSUPPORTED
+    assert f(p, p, None, p, 8, 48, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_EUNSUPPORTED
+    assert f(p, p, None, p, 8, 64, 96, hip.EPI_STORE, *args, 0, None) == hip.SV2_EUNSUPPORTED
+    assert f(p, p, p, p, 8, 64, 48, hip.EPI_SWIGLU, *args, 0, None) == hip.SV2_EUNSUPPORTED
+    assert f(p, p, None, p, 8, 64, 64, 5, *args, 0, None) == hip.SV2_EINVAL
+    assert f(None, p, None, p, 8, 64, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_EINVAL
+    assert f(p, p, None, p, 8, 64, 64, hip.EPI_RESIDUAL, *args, 0, None) == hip.SV2_EINVAL
+    assert f(p, p, None, p, 8, 64, 64, hip.EPI_SWIGLU, *args, 0, None) == hip.SV2_EINVAL
+    assert f(p, p, p, p, 8, 64, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_EINVAL
+    assert f(p, p, p, p, 8, 64, 64, hip.EPI_SWIGLU, p, None, None, None, 0, None) == hip.SV2_EINVAL
+    # a split product without (or with too small) a workspace
+    assert f(p, p, None, p, 58, 2560, 2560, hip.EPI_STORE, None, None, None, None, 0, None) == hip.SV2_EINVAL
+    assert f(p, p, None, p, 58, 2560, 2560, hip.EPI_STORE, None, None, None, p, 1000, None) == hip.SV2_EINVAL
+    assert "workspace" in lib.sv2_last_error().decode()
+    assert f(None, None, None, None, 0, 64, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_OK

@@ -16,6 +16,15 @@ shapes: the DiT block's products at 720p x 21 frames (21600 rows;
 2560 -> 7680, 2560 -> 2560, 2560 -> 2 x 6912, 6912 -> 2560), rows that are
 not a multiple of the 256-row tile, one row, and the unsupported shapes'
 error codes.
+
+The few-row kernel (sv2_inner_product_f16_few, csrc/gemm_few.hip), which
+runs the text branch's products (1-64 rows), is held to the same bars: plain
+products against the float64 product of every row, the bias, gated-residual
+and SwiGLU epilogues against the unfused arithmetic on its own stored
+products, at the text branch's shapes (58 rows; 2560 -> 7680, 2560 -> 2560,
+6912 -> 2560 with K split over 2-6 workgroups, 2560 -> 2 x 6912) and at
+small and ragged ones; a split product's bits do not depend on what its
+workspace held.
 """
 from __future__ import annotations
 
@@ -156,3 +165,106 @@ def test_x_operand_just_under_2gib(hip):
     assert_ulp(got, ref, slack=slack)
     del x, y
     torch.cuda.empty_cache()
+
+
+# ---- the few-row kernel (sv2_inner_product_f16_few, csrc/gemm_few.hip): the
+# text branch's products at 1-64 rows, K split over workgroups with the
+# partial sums added in a fixed order
+
+FEW_SHAPES = [(58, 2560, 7680), (58, 6912, 2560), (58, 2560, 2560), (64, 2560, 2560), (1, 2560, 2560),
+              (17, 512, 128), (33, 64, 64)]
+
+
+@pytest.mark.parametrize("rows,k,n", FEW_SHAPES)
+def test_few_store(hip, rows, k, n):
+    need = hip.load().sv2_inner_product_f16_few_workspace(rows, k, n, hip.EPI_STORE)
+    print(f"[few store] rows={rows} k={k} n={n} workspace={need}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(rows * 7 + k + n)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    y = torch.full((rows, n), float("nan"), dtype=torch.float16, device="cuda")
+    hip.inner_product_f16_few(x, w, y)
+    torch.cuda.synchronize()
+    idx = np.arange(rows)
+    ref, slack = reference64(x, w, idx)
+    mean = assert_ulp(y.cpu().numpy(), ref, slack=slack)
+    assert mean < 2e-4
+    # the bias form: fp16(fp16(x W^T) + bias), bit for bit on the same sums
+    b = torch.randn(n, generator=gen, device="cuda") * 0.1
+    yb = torch.empty_like(y)
+    hip.inner_product_f16_few(x, w, yb, bias=b)
+    torch.cuda.synchronize()
+    v = y.float().cpu().numpy() + b.cpu().numpy()[None, :]
+    assert np.array_equal(yb.cpu().numpy(), v.astype(np.float16))
+
+
+@pytest.mark.parametrize("rows,k", [(58, 2560), (58, 6912), (3, 2560)])
+@pytest.mark.parametrize("bias,gate", [(True, True), (False, True), (True, False)])
+def test_few_residual(hip, rows, k, bias, gate):
+    n = 2560
+    gen = torch.Generator(device="cuda").manual_seed(rows + k + 3)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    r = rand16((rows, n), 1.0, gen)
+    b = torch.randn(n, generator=gen, device="cuda") * 0.1 if bias else None
+    g = torch.randn(n, generator=gen, device="cuda") if gate else None
+    p = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    y = torch.empty_like(p)
+    hip.inner_product_f16_few(x, w, p)
+    hip.inner_product_f16_few(x, w, y, hip.EPI_RESIDUAL, bias=b, gate=g, residual=r)
+    torch.cuda.synchronize()
+    v = p.float().cpu().numpy()
+    if bias:
+        v = v + b.cpu().numpy()[None, :]
+    if gate:
+        v = v * g.cpu().numpy()[None, :]
+    v = v + r.float().cpu().numpy()
+    assert np.array_equal(y.cpu().numpy(), v.astype(np.float16))
+
+
+@pytest.mark.parametrize("rows,k,f", [(58, 2560, 6912), (7, 640, 128), (5, 128, 96)])
+def test_few_swiglu(hip, rows, k, f):
+    """SwiGLU against the unfused formula on the float64 products rounded to
+    fp16.  The fused kernel sums each gate and value product over the whole K
+    in one pass (the plain product of the same shape may split K and add in
+    another order), so g and u may each sit one fp16 ulp from the float64
+    products' roundings: allowed are 3 ulps of the result plus the fp32
+    accumulation allowance carried through silu(g) * u (|silu'| < 1.1)."""
+    gen = torch.Generator(device="cuda").manual_seed(rows + f + 11)
+    x = rand16((rows, k), 1.0, gen)
+    wg = rand16((f, k), 0.02, gen)
+    wu = rand16((f, k), 0.02, gen)
+    y = torch.empty((rows, f), dtype=torch.float16, device="cuda")
+    hip.inner_product_f16_few(x, wg, y, hip.EPI_SWIGLU, w_value=wu)
+    torch.cuda.synchronize()
+    idx = np.arange(rows)
+    g16, sg = reference64(x, wg, idx)
+    u16, su = reference64(x, wu, idx)
+    gg = g16.astype(np.float32)
+    uu = u16.astype(np.float32)
+    silu = gg / (np.float32(1.0) + np.exp(-gg))
+    ref = (silu * uu).astype(np.float16)
+    slack = 1.1 * (sg + ulp16(gg)) * np.abs(uu) + (su + ulp16(uu)) * np.abs(silu)
+    mean = assert_ulp(y.float().cpu().numpy(), ref, ulps=3.0, slack=slack)
+    assert mean < 2e-4
+
+
+def test_few_split_sums_do_not_depend_on_the_workspace(hip):
+    """A split product (58 x 6912 -> 2560: 6 splits) gives the same bits with
+    a fresh workspace, with one filled with NaN bytes beforehand, and on a
+    repeat: the partial sums are overwritten, then added in a fixed order."""
+    rows, k, n = 58, 6912, 2560
+    need = hip.load().sv2_inner_product_f16_few_workspace(rows, k, n, hip.EPI_STORE)
+    assert need > 0
+    gen = torch.Generator(device="cuda").manual_seed(6912)
+    x = rand16((rows, k), 1.0, gen)
+    w = rand16((n, k), 0.02, gen)
+    outs = []
+    for fill in (0, 0xFF, 0xFF):
+        ws = torch.full((need,), fill, dtype=torch.uint8, device="cuda")
+        y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+        hip.inner_product_f16_few(x, w, y, workspace=ws)
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert bool(torch.isfinite(outs[0]).all())
