@@ -282,7 +282,8 @@ def config_table(dev):
                  [(x[1] - x[0]) * (x[3] - x[2]) * (x[5] - x[4])
                   for x in sv2hip.window_plan(sv2hip.rule(Tg, Hg, Wg, False, 2, 8, 10))])
     wbytes = 2 * 2 * (3 * D * D + D * D + 3 * D * DIT_FFN)  # two branches of fp16 matrices
-    rows.append(_row("4", "one block 960+58 tokens, 2x8x10 unshifted, fp16 (InnerProducts on hipBLASLt)",
+    rows.append(_row("4", "one block 960+58 tokens, 2x8x10 unshifted, fp16 (video InnerProducts on hipBLASLt, "
+                     "text rows on the few-row kernel)",
                      ms, gemm + attn_f, wbytes))
     cases.append(dict(kind="block", gpu=gv, weights=w, vid=vid, txt=txt, emb=emb, grid=(Tg, Hg, Wg)))
     return rows, cases
