@@ -690,9 +690,6 @@ try
     float* tab_vm = tables + 3 * D;
     float* tab_ta = tables + 6 * D;
     float* tab_tm = tables + 9 * D;
-    if ((rc = launch_ada_table(emb, vb.ada[1], vb.ada[2], 0, D, tab_va, stream)) != SV2_OK ||
-        (rc = launch_ada_table(emb, vb.ada[4], vb.ada[5], 3, D, tab_vm, stream)) != SV2_OK)
-        return rc;
     const sv2_block_debug* dbg = b->debug_on ? &b->debug : nullptr;
     // With shared weights outside the last layer the text rows get the video
     // rows' treatment in every step but the attention: the same branch (:1139)
@@ -712,16 +709,22 @@ try
     // unmerged fp16 text rows (at most 64) take the few-row InnerProducts
     // with their passes fused; debug captures need the separate passes
     const bool few = Lt > 0 && !merged && !dbg && few_text_products(b, Lt);
-    if (Lt > 0 && !merged &&
-        ((rc = launch_ada_table(emb, tb.ada[1], tb.ada[2], 0, D, tab_ta, stream)) != SV2_OK ||
-         (rc = launch_ada_table(emb, tb.ada[4], tb.ada[5], 3, D, tab_tm, stream)) != SV2_OK))
-        return rc;
+    // the video branch on the fused MFMA InnerProducts (param 14)
+    const bool fused = c.fused_gemm && dt == SV2_F16 && !dbg;
+    // the library path's gated projection adds the bias after the gate
+    const bool gated_bias = !fused && dt == SV2_F16 && !dbg && Lv > 0 && vb.b_proj;
+    // the layer's tables in one launch: video attention and MLP, then the
+    // unmerged text rows' (tab_ta, tab_tm), then the gated bias
+    {
+        const float* scales[4] = {vb.ada[1], vb.ada[4], tb.ada[1], tb.ada[4]};
+        const float* gates[4] = {vb.ada[2], vb.ada[5], tb.ada[2], tb.ada[5]};
+        if ((rc = launch_block_tables(emb, scales, gates, (Lt > 0 && !merged) ? 4 : 2,
+                                      gated_bias ? vb.b_proj : nullptr, D, tables, stream)) != SV2_OK)
+            return rc;
+    }
     // token RMSNorm + ada input; text skips the ada on the last layer (:1141-1151)
     if ((rc = launch_rmsnorm_table(vid, xa, dt, Lr, D, c.norm_eps, tab_va, vb.ada[0], nullptr, 1, stream)) != SV2_OK)
         return rc;
-    // the video branch on the fused MFMA InnerProducts (param 14); unmerged
-    // text rows (a few dozen) stay on the library GEMMs
-    const bool fused = c.fused_gemm && dt == SV2_F16 && !dbg;
     if ((rc = fused ? gemm_mfma(stream, Lr, D, 3 * D, xa, vb.w_qkv, nullptr, qkv_v, kGemmStore, nullptr, nullptr,
                                 nullptr)
                     : gemm_rows(stream, dt, Lr, D, 3 * D, xa, vb.w_qkv, qkv_v)) != SV2_OK)
@@ -805,14 +808,8 @@ try
         rc = SV2_EUNSUPPORTED;
         if (dt == SV2_F16 && !dbg && Lv > 0)
         {
-            float* gated_bias = nullptr;
-            if (vb.b_proj)
-            {
-                gated_bias = tables + 12 * D;
-                if ((rc = launch_gated_bias(tab_va + 2 * D, vb.b_proj, gated_bias, D, stream)) != SV2_OK)
-                    return rc;
-            }
-            rc = gemm_rows_gated(stream, dt, Lr, D, D, att_v, vb.w_proj, p_v, tab_va + 2 * D, vid, gated_bias);
+            rc = gemm_rows_gated(stream, dt, Lr, D, D, att_v, vb.w_proj, p_v, tab_va + 2 * D, vid,
+                                 gated_bias ? tables + 12 * D : nullptr);
             if (rc != SV2_OK && rc != SV2_EUNSUPPORTED)
                 return rc;
         }

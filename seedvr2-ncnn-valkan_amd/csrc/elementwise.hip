@@ -310,14 +310,40 @@ __global__ __launch_bounds__(256) void ada_table_kernel(const float* emb, const 
         out[2 * dim + c] = emb[c * 6 + slot + 2] + gate[c];
 }
 
-// out[c] = gate[c] * bias[c]: an InnerProduct bias moved past the gate, for a
-// product that adds it after its per-channel scaling.
-__global__ __launch_bounds__(256) void gated_bias_kernel(const float* gate, const float* bias, float* out, int dim)
+// Every modulation table of one block in one launch (each a
+// ada_table_kernel table, in the same float operations): tables t = 0 .. n-1
+// of [3][dim] at out + 3 * dim * t, slot 0 for even t (attention) and 3 for
+// odd t (MLP), from scale[t] / gate[t]; then, when bias is not NULL,
+// out[12 * dim + c] = (emb[c*6+2] + gate[0][c]) * bias[c], the video
+// projection's bias moved past its gate (an InnerProduct bias for a product that adds it after its per-channel scaling).
+struct BlockAda
+{
+    const float* scale[4];
+    const float* gate[4];
+    const float* bias;
+    int tables;
+};
+
+__global__ __launch_bounds__(256) void block_tables_kernel(const float* emb, BlockAda a, int dim, float* out)
 {
 #pragma clang fp contract(off)
     const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c < dim)
-        out[c] = gate[c] * bias[c];
+    if (c >= dim)
+        return;
+    for (int t = 0; t < a.tables; t++)
+    {
+        const int slot = (t & 1) ? 3 : 0;
+        float* o = out + static_cast<long long>(3 * t) * dim;
+        o[c] = emb[c * 6 + slot + 1] + a.scale[t][c];
+        o[dim + c] = emb[c * 6 + slot];
+        if (a.gate[t])
+            o[2 * dim + c] = emb[c * 6 + slot + 2] + a.gate[t][c];
+    }
+    if (a.bias)
+    {
+        const float g = emb[c * 6 + 2] + a.gate[0][c];
+        out[12LL * dim + c] = g * a.bias[c];
+    }
 }
 
 // silu(g) * v with silu(g) = g / (1 + exp(-g)) (seedvr2_dit_block.cpp:58-61, :1103-1109).
@@ -602,13 +628,22 @@ int launch_residual(void* x, const void* residual, int dtype, int rows, int dim,
     return err == hipSuccess ? SV2_OK : hip_error(err, "ada_residual_kernel launch");
 }
 
-int launch_gated_bias(const float* gate, const float* bias, float* out, int dim, hipStream_t stream)
+int launch_block_tables(const float* emb, const float* const* scale, const float* const* gate, int tables,
+                        const float* bias, int dim, float* out, hipStream_t stream)
 {
-    if (dim <= 0)
-        return set_error(SV2_EINVAL, "gated_bias: bad dim");
-    hipLaunchKernelGGL(gated_bias_kernel, dim3((dim + 255) / 256), dim3(256), 0, stream, gate, bias, out, dim);
+    if (dim <= 0 || dim % 8 != 0 || tables < 1 || tables > 4 || (bias && !gate[0]))
+        return set_error(SV2_EINVAL, "block_tables: bad dim, table count or bias");
+    BlockAda a{};
+    for (int t = 0; t < tables; t++)
+    {
+        a.scale[t] = scale[t];
+        a.gate[t] = gate[t];
+    }
+    a.bias = bias;
+    a.tables = tables;
+    hipLaunchKernelGGL(block_tables_kernel, dim3((dim + 255) / 256), dim3(256), 0, stream, emb, a, dim, out);
     const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? SV2_OK : hip_error(err, "gated_bias_kernel launch");
+    return err == hipSuccess ? SV2_OK : hip_error(err, "block_tables_kernel launch");
 }
 
 int launch_ada_table(const float* emb, const float* scale, const float* gate, int slot, int dim, float* out,

@@ -134,6 +134,11 @@ int launch_bias_act(void* y, const float* b, int dtype, int rows, int cols, int 
 // emb[c*6+slot+2] + gate[c] (slot 0 attention, 3 MLP).
 int launch_ada_table(const float* emb, const float* scale, const float* gate, int slot, int dim, float* out,
                      hipStream_t stream);
+// A block's tables in one launch: `tables` (1-4) of them at out + 3 * dim * t,
+// slot 0 for even t and 3 for odd t, from scale[t] and gate[t]; with `bias`,
+// out + 12 * dim gets (table 0's gate row) * bias, the gated bias.
+int launch_block_tables(const float* emb, const float* const* scale, const float* const* gate, int tables,
+                        const float* bias, int dim, float* out, hipStream_t stream);
 // Token RMSNorm (times gamma[c] when gamma is not NULL), then when has_ada
 // the input modulation with rows 0-1 of `table` and `shift`.  Arguments
 // already validated (dim a multiple of 8, <= 4096).
@@ -164,8 +169,6 @@ int gemm_f32_exact(hipStream_t stream, int rows, int in, int out, const float* x
 // no kernel for it.  A preceding InnerProduct bias b enters as bias = gate * b.
 int gemm_rows_gated(hipStream_t stream, int dtype, int rows, int in, int out, const void* x, const void* w, void* y,
                     const float* gate, const void* residual, const float* bias = nullptr);
-// out[c] = gate[c] * bias[c] (fp32, dim channels).
-int launch_gated_bias(const float* gate, const float* bias, float* out, int dim, hipStream_t stream);
 
 // fp16 y = epilogue(x W^T) on the hand-written MFMA kernel (gemm.hip), x
 // [rows][in], W (and w2) [out][in].  Epilogues: store; the gated residual
