@@ -153,7 +153,9 @@ int64_t sv2_window_attention_workspace(const sv2_attn_args* args);
  * flash attention of every video window jointly with all text tokens, on
  * gfx950 MFMA; video outputs written once per token (windows partition the
  * grid), text outputs averaged over windows in window order.  Every output
- * element is rounded to bf16 as the reference rounds it (:1074). */
+ * element is rounded to bf16 as the reference rounds it (:1074).  qkv, output
+ * and workspace pointers must be 16-byte aligned (SV2_EINVAL otherwise): the
+ * kernel fetches rows straight into LDS in 16-byte pieces. */
 int sv2_window_attention(const sv2_attn_args* args, void* stream);
 
 /* The three launches of sv2_window_attention, selectable (a bit set of the
@@ -519,7 +521,8 @@ void sv2_dit_destroy(sv2_dit* dit);
  * weight layout); residual fp16 [rows, out]; bias, gate fp32 [out].  Every
  * fp32 step follows the unfused kernels' order.  Requires in % 64 == 0 and
  * out % 256 == 0 (SV2_EPI_SWIGLU: out % 128 == 0); SV2_EUNSUPPORTED
- * otherwise.  y may not alias x, W or residual. */
+ * otherwise.  x, W, W_value, y and residual must be 16-byte aligned
+ * (SV2_EINVAL otherwise).  y may not alias x, W or residual. */
 #define SV2_EPI_STORE 0
 #define SV2_EPI_RESIDUAL 1
 #define SV2_EPI_SWIGLU 2
@@ -537,8 +540,10 @@ int sv2_inner_product_f16(const void* x, const void* w, const void* w_value, voi
  * split the partial sums go to `workspace` (device memory of at least
  * sv2_inner_product_f16_few_workspace() bytes; 0 bytes: none needed, NULL
  * allowed); they are added in a fixed order, so results do not depend on
- * timing.  Calls that share a workspace must not overlap.  y may not alias
- * x, W, residual or the workspace. */
+ * timing.  Calls that share a workspace must not overlap.  x, W, W_value
+ * and the workspace must be 16-byte aligned, y and residual 8-byte aligned
+ * (SV2_EINVAL otherwise).  y may not alias x, W, residual or the
+ * workspace. */
 int64_t sv2_inner_product_f16_few_workspace(int rows, int in, int out, int epilogue);
 int sv2_inner_product_f16_few(const void* x, const void* w, const void* w_value, void* y, int rows, int in, int out,
                               int epilogue, const float* bias, const float* gate, const void* residual,

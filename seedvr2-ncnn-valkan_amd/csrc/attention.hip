@@ -2123,6 +2123,9 @@ int prepare(const sv2_attn_args* a, AttnParams* p, int* smax_out, int* vmax_out,
         return set_error(SV2_EINVAL, "attention: unknown rope mode");
     if (!a->vid_qkv || (a->text_len > 0 && !a->txt_qkv))
         return set_error(SV2_EINVAL, "attention: null qkv pointer");
+    if (misaligned(a->vid_qkv, 16) || (a->text_len > 0 && misaligned(a->txt_qkv, 16)) ||
+        misaligned(a->vid_out, 16) || (a->text_len > 0 && misaligned(a->txt_out, 16)))
+        return set_error(SV2_EINVAL, "attention: qkv and output pointers must be 16-byte aligned");
     if (a->qk_norm && (!a->gamma_q_vid || !a->gamma_k_vid))
         return set_error(SV2_EINVAL, "attention: qk_norm needs the video gamma vectors");
     if (a->exact && a->qkv_dtype != SV2_F32)
@@ -2212,6 +2215,8 @@ int bind_workspace(const sv2_attn_args* a, AttnParams* p)
     const Workspace w = workspace_layout(*p);
     if (w.total > 0 && (!a->workspace || static_cast<int64_t>(a->workspace_bytes) < w.total))
         return set_error(SV2_EINVAL, "attention: workspace missing or too small");
+    if (w.total > 0 && misaligned(a->workspace, 16))
+        return set_error(SV2_EINVAL, "attention: workspace must be 16-byte aligned");
     char* base = static_cast<char*>(a->workspace);
     p->partial = reinterpret_cast<uint16_t*>(base + w.partial);
     p->txt_q = reinterpret_cast<uint16_t*>(base + w.txt_q);

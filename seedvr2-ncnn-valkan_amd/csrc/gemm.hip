@@ -448,6 +448,8 @@ int gemm_mfma(hipStream_t stream, int rows, int in, int out, const void* x, cons
                          "inner product: needs in a multiple of 64 and out a multiple of 256 (SwiGLU: 128)");
     if (!x || !w || !y || (epi == kResidual && !residual) || (epi == kSwiGLU && !w2))
         return set_error(SV2_EINVAL, "inner product: null pointer");
+    if (misaligned(x, 16) || misaligned(w, 16) || misaligned(w2, 16) || misaligned(y, 16) || misaligned(residual, 16))
+        return set_error(SV2_EINVAL, "inner product: x, W, y and residual must be 16-byte aligned");
     // the operands are read through buffer resources with 32-bit byte offsets
     // (the kernel forms them unsigned, so padded tile rows past `rows` stay
     // exact; see make_operands)

@@ -357,6 +357,10 @@ int gemm_few(hipStream_t stream, int rows, int in, int out, const void* x, const
         return set_error(SV2_EINVAL, "few-row inner product: null pointer");
     if (epi == kGemmSwiGLU && (bias || gate))
         return set_error(SV2_EINVAL, "few-row inner product: SwiGLU takes no bias or gate");
+    if (misaligned(x, 16) || misaligned(w, 16) || misaligned(w2, 16) || misaligned(y, 8) || misaligned(residual, 8) ||
+        misaligned(work, 16))
+        return set_error(SV2_EINVAL, "few-row inner product: x, W and the workspace must be 16-byte aligned, y and "
+                                     "residual 8-byte aligned");
     const int splits = gemm_few_splits(rows, in, out, epi);
     const size_t need = gemm_few_workspace(rows, in, out, epi);
     if (need > 0 && (!work || work_bytes < need))

@@ -101,6 +101,13 @@ __host__ __device__ inline float bf16_round(float value)
 
 // Thread-local error message plumbing for the C ABI.
 int set_error(int code, const std::string& message);
+// True for a non-null pointer that is not `bytes`-aligned (bytes a power of
+// two): operands fetched by 16-byte vector loads or straight into LDS are
+// refused rather than read at the wrong address.
+inline bool misaligned(const void* ptr, uintptr_t bytes)
+{
+    return ptr && (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) != 0;
+}
 int hip_error(hipError_t err, const char* what);
 // Called from the catch clause of an entry point of the C ABI, which lets no
 // C++ exception out (std::bad_alloc of a host container, std::system_error

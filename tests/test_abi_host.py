@@ -263,3 +263,34 @@ def test_few_row_inner_product_checks(hip):
     assert f(p, p, None, p, 58, 2560, 2560, hip.EPI_STORE, None, None, None, p, 1000, None) == hip.SV2_EINVAL
     assert "workspace" in lib.sv2_last_error().decode()
     assert f(None, None, None, None, 0, 64, 64, hip.EPI_STORE, *args, 0, None) == hip.SV2_OK
+
+
+def test_misaligned_device_pointers_are_refused(hip):
+    """Operands the kernels fetch straight into LDS (or with 16-byte vector
+    loads) must be aligned: a misaligned qkv, output or workspace pointer of
+    the attention, or operand of the InnerProducts, is refused before any
+    launch (these dummy addresses are never touched)."""
+    lib = hip.load()
+    a16, a8, odd = 4096, 4104, 4098
+    f = lib.sv2_inner_product_f16
+    assert f(odd, a16, None, a16, 4, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EINVAL
+    assert f(a16, a8, None, a16, 4, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EINVAL
+    assert f(a16, a16, None, a8, 4, 64, 256, hip.EPI_STORE, None, None, None, None) == hip.SV2_EINVAL
+    assert "aligned" in lib.sv2_last_error().decode()
+    g = lib.sv2_inner_product_f16_few
+    assert g(a8, a16, None, a16, 4, 64, 64, hip.EPI_STORE, None, None, None, None, 0, None) == hip.SV2_EINVAL
+    assert g(a16, a16, None, odd, 4, 64, 64, hip.EPI_STORE, None, None, None, None, 0, None) == hip.SV2_EINVAL
+    assert g(a16, a16, None, a16, 4, 64, 64, hip.EPI_RESIDUAL, None, None, odd, None, 0, None) == hip.SV2_EINVAL
+    assert "aligned" in lib.sv2_last_error().decode()
+    # attention: the size query takes any 16-byte-aligned placeholder, and
+    # refuses a misaligned qkv pointer
+    args = hip.AttnArgs()
+    args.rule = hip.rule(2, 16, 30, False, 2, 8, 10)
+    args.heads, args.head_dim, args.text_len = 2, 128, 8
+    args.eps, args.qk_norm, args.rope_mode = 1e-5, 0, hip.ROPE_NONE
+    args.qkv_dtype = args.out_dtype = hip.F16
+    args.vid_qkv = args.txt_qkv = a16
+    assert lib.sv2_window_attention_workspace(ctypes.byref(args)) >= 0
+    args.txt_qkv = a8
+    assert lib.sv2_window_attention_workspace(ctypes.byref(args)) == hip.SV2_EINVAL
+    assert "aligned" in lib.sv2_last_error().decode()
