@@ -139,6 +139,9 @@ SMALL_VARIANTS = [
     ("fixed_windows_shifted", {"window_t": 2, "window_h": 4, "window_w": 6, "shifted_window": 1}, (3, 8, 12), 5),
     ("absolute_rope", {"rope_mode": 1, "window_t": 2, "window_h": 4, "window_w": 6}, (2, 8, 12), 6),
     ("no_rope_no_norm", {"rope_mode": 2, "qk_norm": 0}, (2, 6, 10), 4),
+    # fp16 text rows up to 64 take the few-row InnerProducts, 65 the library's
+    ("text_64", {}, (2, 6, 10), 64),
+    ("text_65", {}, (2, 6, 10), 65),
     ("no_text", {}, (2, 6, 10), 0),
 ]
 
