@@ -268,3 +268,51 @@ def test_few_split_sums_do_not_depend_on_the_workspace(hip):
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     assert bool(torch.isfinite(outs[0]).all())
+
+
+def test_few_random_shapes(hip):
+    """A seeded sweep of few-row shapes (1-64 rows, K 64-4096, N 64-3072, every
+    epilogue, K split or not) against the float64 product: store within one
+    fp16 ulp plus the accumulation allowance, the residual bit for bit on the
+    kernel's own stored product, SwiGLU within 3 ulps plus the carried
+    allowance."""
+    rng = np.random.default_rng(2024)
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    lib = hip.load()
+    for case in range(24):
+        rows = int(rng.integers(1, 65))
+        k = 64 * int(rng.integers(1, 65))
+        epi = [hip.EPI_STORE, hip.EPI_RESIDUAL, hip.EPI_SWIGLU][case % 3]
+        n = (32 if epi == hip.EPI_SWIGLU else 64) * int(rng.integers(1, 49))
+        splits = max(1, lib.sv2_inner_product_f16_few_workspace(rows, k, n, epi) // (rows * n * 4))
+        print(f"[few sweep] case {case}: rows={rows} k={k} n={n} epi={epi} splits={splits}", flush=True)
+        x = rand16((rows, k), 1.0, gen)
+        w = rand16((n, k), 0.02, gen)
+        idx = np.arange(rows)
+        ref, slack = reference64(x, w, idx)
+        y = torch.full((rows, n), float("nan"), dtype=torch.float16, device="cuda")
+        if epi == hip.EPI_STORE:
+            hip.inner_product_f16_few(x, w, y)
+            torch.cuda.synchronize()
+            assert_ulp(y.cpu().numpy(), ref, slack=slack)
+        elif epi == hip.EPI_RESIDUAL:
+            r = rand16((rows, n), 1.0, gen)
+            b = torch.randn(n, generator=gen, device="cuda") * 0.1
+            g = torch.randn(n, generator=gen, device="cuda")
+            p = torch.empty_like(y)
+            hip.inner_product_f16_few(x, w, p)
+            hip.inner_product_f16_few(x, w, y, hip.EPI_RESIDUAL, bias=b, gate=g, residual=r)
+            torch.cuda.synchronize()
+            assert_ulp(p.cpu().numpy(), ref, slack=slack)
+            v = (p.float().cpu().numpy() + b.cpu().numpy()[None, :]) * g.cpu().numpy()[None, :] + r.float().cpu().numpy()
+            assert np.array_equal(y.cpu().numpy(), v.astype(np.float16))
+        else:
+            wu = rand16((n, k), 0.02, gen)
+            hip.inner_product_f16_few(x, w, y, hip.EPI_SWIGLU, w_value=wu)
+            torch.cuda.synchronize()
+            u16, su = reference64(x, wu, idx)
+            gg = ref.astype(np.float32)
+            uu = u16.astype(np.float32)
+            silu = gg / (np.float32(1.0) + np.exp(-gg))
+            sl = 1.1 * (slack + ulp16(gg)) * np.abs(uu) + (su + ulp16(uu)) * np.abs(silu)
+            assert_ulp(y.float().cpu().numpy(), (silu * uu).astype(np.float16), ulps=3.0, slack=sl)
