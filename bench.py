@@ -218,7 +218,8 @@ def config_table(dev):
     that fits a GPU and the CPU beside it: the single windowed MM-attention
     layer at the 480x256x5 grid 2x16x30 (config 1: fp32, no RoPE, no QK-norm,
     2x8x10 unshifted windows; config 2: fp16, QK-RMSNorm + RoPE, unshifted and
-    shifted) and one DiT block at that grid (config 4: hidden 2560, 20 heads,
+    shifted, and bf16 unshifted, whose P*V takes P as two bf16 terms) and one
+    DiT block at that grid (config 4: hidden 2560, 20 heads,
     MLP 6912, fp16 weights N(0, 0.02^2), fp16 inputs N(0, 1), 58 text tokens).
     GPU ms: mean over 20 launches after 3 warmups (HIP events).  Config 3 is
     the line's own workload; config 5 the dit_step.
@@ -233,10 +234,11 @@ def config_table(dev):
     Lv = Tg * Hg * Wg
     freqs = reference_freqs()
     rows, cases = [], []
-    tdt = {"f32": torch.float32, "f16": torch.float16}
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
     for name, in_dt, norm, rope, shifted in (("1", "f32", False, sv2hip.ROPE_NONE, False),
                                              ("2", "f16", True, sv2hip.ROPE_REFERENCE, False),
-                                             ("2", "f16", True, sv2hip.ROPE_REFERENCE, True)):
+                                             ("2", "f16", True, sv2hip.ROPE_REFERENCE, True),
+                                             ("2", "bf16", True, sv2hip.ROPE_REFERENCE, False)):
         rng = np.random.default_rng(31 + shifted)
         vid = cast_like(rng.standard_normal((Lv, 3 * D), dtype=np.float32), in_dt)
         txt = cast_like(rng.standard_normal((L_TXT, 3 * D), dtype=np.float32), in_dt)
